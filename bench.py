@@ -1,0 +1,216 @@
+#!/usr/bin/env python3
+"""Benchmark of the hot path: batched C2C FFT, N=1024, batch 65536 (config 2).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+One step = one ThunderFFT_global launch (the C ABI's asynchronous entry,
+thff_global_async) over the whole batch, inputs resident in HBM.  Prints one
+JSON line: value = GFLOP/s (5 N log2 N per transform) of the float forward
+transform; the half and inverse transforms are reported under "also".
+roofline.achieved = algorithmic bytes per launch (read + write of every
+complex value once: 2 * batch * N * sizeof(T)) / mean kernel duration, the
+duration measured with HIP events recorded around each launch on the launch
+stream.  cpu_baseline = the oracle's fp32 four-step port (the reference has no
+CPU path) timed on this host's cores on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+HBM_PEAK_GBPS = 8000.0
+N_FFT = 1024
+BATCH = 65536
+PROFILE_TRAFFIC = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "traffic_c2c_n1024.json")
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="target wall time of the CPU baseline sample")
+    return ap.parse_args()
+
+
+def time_gpu(T: str, forward: bool, steps: int, warmup: int) -> dict:
+    import torch
+
+    import thunderfft_amd as thff
+
+    n, batch = N_FFT, BATCH
+    dt = torch.float32 if T == "float" else torch.float16
+    elem = 8 if T == "float" else 4
+    x = torch.empty(2 * n * batch, dtype=dt, device="cuda")
+    y = torch.empty_like(x)
+    stream = torch.cuda.current_stream()
+    thff.fill_uniform(T, x, n * batch, 0x7F4A7C15 + n, 0, stream)
+    thff.ThunderFFTInitialize(T, n)
+    for _ in range(warmup):
+        thff.ThunderFFT_global_async(T, n, forward, x, y, batch, stream)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        thff.ThunderFFT_global_async(T, n, forward, x, y, batch, stream)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))  # ms
+    mean_ms = sum(per) / len(per)
+    median_ms = per[len(per) // 2]
+    nbytes = 2 * n * batch * elem
+    flops = 5.0 * n * math.log2(n) * batch
+    del x, y
+    return {
+        "precision": T, "direction": "forward" if forward else "inverse",
+        "us_per_call": mean_ms * 1e3, "us_per_call_median": median_ms * 1e3,
+        "us_per_transform": mean_ms * 1e3 / batch,
+        "gflops": flops / (mean_ms * 1e-3) / 1e9,
+        "gbps": nbytes / (mean_ms * 1e-3) / 1e9,
+        "pct_hbm_peak": 100.0 * nbytes / (mean_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+        "bytes_per_call": nbytes, "wall_s": wall,
+    }
+
+
+def copy_bandwidth() -> float:
+    """Device-to-device copy of a 512 MiB buffer (read + write), GB/s."""
+    import torch
+
+    a = torch.empty(64 << 20, dtype=torch.float64, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1.0)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 20
+    s.record()
+    for _ in range(reps):
+        b.copy_(a)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / reps
+    del a, b
+    return 2 * (64 << 20) * 8 / (ms * 1e-3) / 1e9
+
+
+def cpu_baseline(target_s: float) -> dict:
+    """The oracle's fp32 four-step (restating the reference's radix-4 64x16
+    split) on this host's cores, on a bounded sample of the N=1024 workload."""
+    import numpy as np
+
+    import oracle
+
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = max(1, min(int(cores or 1), 64))
+    n = N_FFT
+    sample = 1024
+    x = oracle.uniform(n, sample)
+    oracle.fft_f32_fourstep(x, True, cores)  # warm
+    # grow the sample until one timed pass takes a meaningful share of target_s
+    while True:
+        x = oracle.uniform(n, sample)
+        t0 = time.perf_counter()
+        oracle.fft_f32_fourstep(x, True, cores)
+        dt = time.perf_counter() - t0
+        if dt >= target_s / 4 or sample >= BATCH:
+            break
+        sample = min(BATCH, sample * max(2, int(target_s / 4 / max(dt, 1e-3))))
+    reps = max(1, int(target_s / max(dt, 1e-3)))
+    reps = min(reps, 8)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        oracle.fft_f32_fourstep(x, True, cores)
+    dt = (time.perf_counter() - t0) / reps
+    flops = 5.0 * n * math.log2(n) * sample
+    del x
+    return {"value": flops / dt / 1e9, "unit": "GFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"{sample} float forward transforms of N={n} (of the {BATCH}-signal "
+                      f"workload), {reps} timed passes, {dt * 1e3:.1f} ms per pass, "
+                      f"oracle fft_f32_fourstep",
+            "us_per_transform": dt * 1e6 / sample}
+
+
+def load_traffic():
+    try:
+        with open(PROFILE_TRAFFIC) as f:
+            d = json.load(f)
+        return d.get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    a = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print("bench.py: this build measures one GPU only; the batched transform shards "
+              "over GPUs by splitting the batch (see DESIGN.md). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import thunderfft_amd as thff
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    thff.lib()
+    runs = {}
+    for T in ("float", "half"):
+        for fwd in (True, False):
+            r = time_gpu(T, fwd, a.steps, a.warmup)
+            runs[f"{T}_{'fwd' if fwd else 'inv'}"] = r
+            print(f"[bench] {T} {'forward' if fwd else 'inverse'}: {r['us_per_call']:.1f} us, "
+                  f"{r['gbps']:.0f} GB/s ({r['pct_hbm_peak']:.1f}% of HBM peak), "
+                  f"{r['gflops']:.0f} GFLOP/s", file=sys.stderr, flush=True)
+    thff.ThunderFFTFinalize("float")
+    thff.ThunderFFTFinalize("half")
+    copy_gbps = copy_bandwidth()
+    main_run = runs["float_fwd"]
+    cpu = None if a.no_cpu else cpu_baseline(a.cpu_seconds)
+    achieved = main_run["gbps"]
+    out = {
+        "metric": "C2C FFT µs, GFLOP/s and % HBM peak at N=1024 b=65536 (fp32/fp16)",
+        "value": round(main_run["gflops"], 2),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(main_run["us_per_call"] / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded counter-based U[-1,1) complex inputs generated on device",
+        "config": {"workload": "batched C2C FFT float2 forward, N=1024, batch=65536, "
+                               "out-of-place", "n": N_FFT, "batch": BATCH,
+                   "precision": "float2 storage, fp32 arithmetic"},
+        "us_per_call": round(main_run["us_per_call"], 3),
+        "pct_hbm_peak": round(main_run["pct_hbm_peak"], 2),
+        "pct_copy_bw": round(100.0 * achieved / copy_gbps, 2),
+        "copy_gbps": round(copy_gbps, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": load_traffic(),
+                     "kernel": "thff::c2c_kernel<float2,1024,true>",
+                     "algorithmic_bytes": main_run["bytes_per_call"]},
+        "cpu_baseline": cpu,
+        "also": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
+                     for kk, vv in v.items()} for k, v in runs.items()},
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

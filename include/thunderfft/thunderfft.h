@@ -1,0 +1,103 @@
+/*
+ * thunderfft.h -- C ABI of the MI355X (gfx950) ThunderFFT library
+ * (libthunderfft_amd.so).
+ *
+ * The reference (mcrl/thunderfft) is a header-only CUDA C++ template API with
+ * no C ABI.  Each entry point below is the plain-pointer form of one
+ * reference interface, cited as path:line in the reference tree; the C++
+ * template API of the reference is restated on top of these entry points in
+ * <thunderfft/thunderfft.hpp>.  No PyTorch or HIP types appear in the
+ * signatures: streams are passed as `void*` (a hipStream_t, NULL = the null
+ * stream) and buffers as device pointers.
+ *
+ * Return codes: THFF_OK on success; THFF_EINVAL where the reference throws
+ * std::invalid_argument (always before any HIP call); THFF_EIO where it
+ * throws std::runtime_error("[ThunderFFT] ...").  thff_last_error() returns
+ * the message of the calling thread's last failure.
+ */
+#ifndef THUNDERFFT_AMD_THUNDERFFT_H
+#define THUNDERFFT_AMD_THUNDERFFT_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define THFF_OK 0
+#define THFF_EINVAL (-22)
+#define THFF_EIO (-5)
+
+/* Component type T of the reference templates: float (float2 storage) or
+ * half (__half2 storage, low = real, high = imaginary). */
+#define THFF_FLOAT 0
+#define THFF_HALF 1
+
+/* Library version, major*10000 + minor*100 + patch. */
+int thff_version(void);
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* thff_last_error(void);
+
+/* ThunderFFTInitialize<T>(N)
+ *   reference: include/thunderfft/thunderfft.cuh:55-56,
+ *              include/thunderfft/detail/thunderfft_impl_twiddle.cuh:279-327.
+ * Builds (or keeps, if it already holds N) the current device's twiddle table
+ * for `precision`: N fp32 complex values W[m] = (cos, sin)(2*pi*m/N), computed
+ * in fp64 and rounded once.  One N per (device, precision); another N
+ * replaces it.  N outside {64,...,4096} (powers of two) -> THFF_EINVAL before
+ * any HIP call.  Serialised per precision; not stream ordered: finish every
+ * transform that uses the old table before replacing it. */
+int thff_initialize(int precision, int n);
+
+/* ThunderFFTFinalize<T>()
+ *   reference: include/thunderfft/thunderfft.cuh:62-63,
+ *              include/thunderfft/detail/thunderfft_impl_twiddle.cuh:358-378.
+ * Frees the current device's table for `precision`; a second call is a no-op.
+ * Other devices' tables are untouched. */
+int thff_finalize(int precision);
+
+/* ThunderFFT_global<T,N,forward>(d_input, d_output, batch, stream)
+ *   reference: include/thunderfft/thunderfft.cuh:150-154,
+ *              include/thunderfft/detail/thunderfft_impl_kernel.cuh:6-41.
+ * Batched, unnormalized, out-of-place C2C transforms of `batch` contiguous
+ * natural-order signals of n complex values (signal b at offset b*n).
+ * forward != 0 uses exp(-2*pi*i*n*k/N), forward == 0 exp(+...).
+ * Argument checks in the reference's order, all before any HIP call:
+ *   unsupported precision or n -> THFF_EINVAL (a static_assert there);
+ *   batch < 0 -> THFF_EINVAL; batch == 0 -> THFF_OK without touching the
+ *   pointers; null d_input or d_output, or d_input == d_output -> THFF_EINVAL.
+ * Requires thff_initialize(precision, n) on the current device (THFF_EIO
+ * otherwise).  Synchronises `stream` before returning, like the reference. */
+int thff_global(int precision, int n, int forward, const void* d_input, void* d_output,
+                int batch, void* stream);
+
+/* Same as thff_global without the final stream synchronisation: the launch is
+ * enqueued on `stream` and the call returns.  No counterpart in the
+ * reference (whose wrapper always synchronises); for callers that time or
+ * pipeline transforms.  Same checks and return codes. */
+int thff_global_async(int precision, int n, int forward, const void* d_input, void* d_output,
+                      int batch, void* stream);
+
+/* Snapshot of the current device's twiddle cache for `precision`: the device
+ * pointer (NULL when released) and its length (0 when released).  The
+ * reference exposes the same state through its device symbols
+ * d_twiddle_{f,h} / d_twiddle_N_{f,h}
+ * (include/thunderfft/detail/thunderfft_impl_twiddle.cuh:44-68), read by
+ * sample/validation/cache_validation.cu:36-50.  Entries are fp32 complex
+ * (8 bytes) for both precisions. */
+int thff_twiddle_info(int precision, const void** d_table, int* n);
+
+/* Benchmark/test input generator (no reference counterpart; the reference
+ * seeds its inputs on the host or with an LCG kernel,
+ * sample/bench/paper_fft.cu:27-43).  Writes `count` complex values to
+ * d_out in `precision` storage: component c (real of element e is
+ * c = 2*(first_element + e), imaginary c + 1) is
+ * 2 * (splitmix64(seed ^ c) >> 40) * 2^-24 - 1, exact in fp32, rounded to
+ * nearest-even for half.  Asynchronous on `stream`. */
+int thff_fill_uniform(int precision, void* d_out, long long count, unsigned long long seed,
+                      long long first_element, void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* THUNDERFFT_AMD_THUNDERFFT_H */

@@ -1,0 +1,88 @@
+// thunderfft.hpp -- the reference's C++ host API on MI355X (gfx950).
+//
+// Same names, template parameters, argument order, synchronous semantics and
+// exception contract as mcrl/thunderfft's include/thunderfft/thunderfft.cuh
+// (:55-56 ThunderFFTInitialize, :62-63 ThunderFFTFinalize, :150-154
+// ThunderFFT_global) and detail/util_cuda.h:46-49 (vec2_t).  Each call
+// forwards to the C ABI of libthunderfft_amd.so (thunderfft/thunderfft.h) and
+// turns its return code into the reference's exception:
+//   THFF_EINVAL -> std::invalid_argument (raised before any HIP call)
+//   THFF_EIO    -> std::runtime_error("[ThunderFFT] <context>: <hip error>")
+// Differences from the reference: the stream is a hipStream_t, and a
+// ThunderFFT_global<T,N> call on a device whose twiddle cache for T does not
+// hold N throws std::runtime_error instead of running without it.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <stdexcept>
+#include <string>
+#include <type_traits>
+
+#include "thunderfft/thunderfft.h"
+
+template <class T>
+using vec2_t = typename std::conditional_t<std::is_same_v<std::remove_cv_t<T>, float>, float2,
+                                           half2>;
+
+namespace thunderfft {
+
+namespace detail {
+
+template <class T>
+constexpr int precision_code() {
+    static_assert(std::is_same_v<T, float> || std::is_same_v<T, half>,
+                  "ThunderFFT supports float and half only");
+    return std::is_same_v<T, float> ? THFF_FLOAT : THFF_HALF;
+}
+
+inline void check(int rc) {
+    if (rc == THFF_OK) return;
+    if (rc == THFF_EINVAL) throw std::invalid_argument(thff_last_error());
+    throw std::runtime_error(thff_last_error());
+}
+
+}  // namespace detail
+
+// Supported transform lengths (include/thunderfft/thunderfft.cuh:20-23,145).
+template <int N>
+inline constexpr bool is_supported_length =
+    N == 64 || N == 128 || N == 256 || N == 512 || N == 1024 || N == 2048 || N == 4096;
+
+// Transforms per workgroup of the global kernel (the reference's
+// batch_per_block<N>, detail/thunderfft_impl.cuh:14-22; wave64 values).
+template <int N>
+inline constexpr int batch_per_block = is_supported_length<N> ? 4096 / N : 0;
+
+// Lanes per wavefront on gfx950 (the reference's threads_per_warp = 32).
+inline constexpr int threads_per_warp = 64;
+
+// Initialise the current device's twiddle table for (T, N).  Unsupported N
+// throws std::invalid_argument before any HIP call; one N per (device, T).
+template <typename T>
+void ThunderFFTInitialize(int N) {
+    detail::check(thff_initialize(detail::precision_code<T>(), N));
+}
+
+// Release the current device's twiddle table for T (repeat calls are fine).
+template <typename T>
+void ThunderFFTFinalize() {
+    detail::check(thff_finalize(detail::precision_code<T>()));
+}
+
+// Batched unnormalized out-of-place C2C FFT of `batch` natural-order signals
+// of N values (signal j at offset j*N).  forward = exp(-2*pi*i*k/N).
+// batch < 0, null or identical pointers throw std::invalid_argument; batch 0
+// is a no-op.  Synchronises `stream` before returning.
+template <typename T, int N, bool forward = true>
+inline void ThunderFFT_global(vec2_t<T>* d_input, vec2_t<T>* d_output, int batch,
+                              hipStream_t stream = 0) {
+    static_assert(std::is_same_v<T, float> || std::is_same_v<T, half>,
+                  "ThunderFFT_global supports float and half only");
+    static_assert(is_supported_length<N>, "Unsupported ThunderFFT length");
+    detail::check(thff_global(detail::precision_code<T>(), N, forward ? 1 : 0, d_input, d_output,
+                              batch, static_cast<void*>(stream)));
+}
+
+}  // namespace thunderfft

@@ -1,0 +1,220 @@
+"""GPU parity of ThunderFFT_global against the fp64 oracle, through the C ABI.
+
+Restates the reference's correctness matrix (sample/validation/
+fft_validation.cu:194-311): every size x {float, half} x {forward, inverse}
+x the four input kinds, full batch 64 and public tail batches {1, BPB-1,
+BPB+1} (BPB = transforms per workgroup here), NaN-prefilled outputs with 16
+trailing sentinels that must survive, inputs allocated exactly batch*N long,
+reference = fp64 transform of the values the storage type represents.
+Pass = finite, relative L2 <= 5e-3 (the reference's gate) and within this
+build's tighter fp32-arithmetic bar (TIGHT).  The full-size configurations
+are checked on a subset of signals against the oracle and over every signal
+through the unnormalized round trip inverse(forward(x)) = N*x.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from thff_testlib import GATE, SIZES, TIGHT, from_device, run_case, to_device
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "c2c_numpy.npz")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    import torch
+
+    import thunderfft_amd as thff
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    thff.lib()
+    yield
+    thff.ThunderFFTFinalize("float")
+    thff.ThunderFFTFinalize("half")
+
+
+def _tails(n):
+    import thunderfft_amd as thff
+
+    bpb = thff.transforms_per_block(n)
+    return sorted({b for b in (1, bpb - 1, bpb + 1) if b > 0 and b != 64})
+
+
+def _check(m, T, label):
+    print(f"{label}: rel_l2={m['rel_l2']:.3e} rel_linf={m['rel_linf']:.3e} "
+          f"guards={m['guards_changed']}", flush=True)
+    assert m["nonfinite"] == 0, label
+    assert m["guards_changed"] == 0, label
+    assert m["rel_l2"] <= GATE, label
+    assert m["rel_l2"] <= TIGHT[T], label
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("n", SIZES)
+def test_validation_matrix(T, n):
+    for kind in range(4):
+        for forward in (True, False):
+            for batch in [64] + _tails(n):
+                x = oracle.make_input(n, batch, kind)
+                m = run_case(T, n, forward, x)
+                _check(m, T, f"{T} N={n} {'fwd' if forward else 'inv'} "
+                             f"{oracle.INPUT_KINDS[kind]} batch={batch}")
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+def test_golden_fixtures(T):
+    """Config 1 (N=64, batch 16, float forward) and one signal of every other
+    length against numpy.fft spectra of the fixture inputs."""
+    g = np.load(GOLDEN)
+    for key in g.files:
+        if not key.endswith("_x"):
+            continue
+        x = g[key]
+        n = x.shape[-1]
+        for forward, tag in ((True, "fwd"), (False, "inv")):
+            m = run_case(T, n, forward, x)
+            if T == "float":
+                # float storage represents the fixture input exactly
+                m2 = oracle.metrics(m["out"], g[key[:-2] + "_" + tag])
+                assert m2["rel_l2"] <= TIGHT[T], key
+                assert m2["rel_linf"] <= 10 * TIGHT[T], key
+            _check(m, T, f"golden {key} {tag}")
+
+
+def test_reinitialize_after_finalize():
+    """fft_validation.cu:302-310: finalize, re-initialize at 64, transform again."""
+    import thunderfft_amd as thff
+
+    for T in ("float", "half"):
+        thff.ThunderFFTInitialize(T, 4096)
+        thff.ThunderFFTFinalize(T)
+        thff.ThunderFFTInitialize(T, 64)
+        for forward in (True, False):
+            m = run_case(T, 64, forward, oracle.make_input(64, 1, 0))
+            _check(m, T, f"reinit {T} {forward}")
+
+
+def test_uninitialized_length_raises():
+    import torch
+
+    import thunderfft_amd as thff
+
+    thff.ThunderFFTInitialize("float", 64)
+    x = torch.zeros(2 * 128, device="cuda")
+    y = torch.zeros(2 * 128, device="cuda")
+    with pytest.raises(RuntimeError, match=r"\[ThunderFFT\].*ThunderFFTInitialize<float>\(128\)"):
+        thff.ThunderFFT_global("float", 128, True, x, y, 1)
+
+
+def test_twiddle_cache_lifecycle():
+    """sample/validation/cache_validation.cu:65-121 on the current device."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    for T in ("float", "half"):
+        thff.ThunderFFTFinalize(T)
+        assert thff.twiddle_info(T) == (0, 0)
+        thff.ThunderFFTInitialize(T, 64)
+        p64, n = thff.twiddle_info(T)
+        assert p64 != 0 and n == 64
+        thff.ThunderFFTInitialize(T, 64)
+        assert thff.twiddle_info(T) == (p64, 64), "same-length init must keep the allocation"
+        thff.ThunderFFTInitialize(T, 128)
+        p128, n = thff.twiddle_info(T)
+        assert n == 128 and p128 != 0
+        # read W[0], W[1] back through a device-to-device copy into a torch tensor
+        buf = torch.empty(4, dtype=torch.float32, device="cuda")
+        import ctypes
+        hip = ctypes.CDLL("libamdhip64.so")
+        hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        assert hip.hipMemcpy(buf.data_ptr(), p128, 16, 3) == 0  # hipMemcpyDeviceToDevice
+        w = buf.cpu().numpy()
+        assert w[0] == 1.0 and w[1] == 0.0, "W[0] must be 1+0i"
+        assert abs(w[2] - np.cos(2 * np.pi / 128)) <= 1e-6
+        assert abs(w[3] - np.sin(2 * np.pi / 128)) <= 1e-6
+        thff.ThunderFFTFinalize(T)
+        assert thff.twiddle_info(T) == (0, 0)
+        thff.ThunderFFTFinalize(T)  # repeated finalize is fine
+        assert thff.twiddle_info(T) == (0, 0)
+        thff.ThunderFFTInitialize(T, 64)
+        assert thff.twiddle_info(T)[1] == 64
+        thff.ThunderFFTFinalize(T)
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+def test_device_generator_matches_oracle(T):
+    import torch
+
+    import thunderfft_amd as thff
+
+    n, batch, first = 1024, 7, 12345
+    d = torch.empty(n * batch * (2 if T == "float" else 2), device="cuda",
+                    dtype=torch.float32 if T == "float" else torch.float16)
+    thff.fill_uniform(T, d, n * batch, oracle.BENCH_SEED_BASE + n, first)
+    torch.cuda.synchronize()
+    got = from_device(d, T).reshape(batch, n)
+    want = oracle.represent(oracle.uniform(n, batch, first_element=first), T)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def _subset_rows(batch, k=256):
+    rows = np.unique(np.concatenate([np.linspace(0, batch - 1, k).astype(np.int64),
+                                     np.arange(max(0, batch - 5), batch)]))
+    return rows
+
+
+def _large_case(T, n, batch, directions=(True, False)):
+    """Full-size case: device-generated seeded input, oracle check on a subset of
+    signals, round trip over every signal."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    dt = torch.float32 if T == "float" else torch.float16
+    count = n * batch
+    seed = oracle.BENCH_SEED_BASE + n
+    x = torch.empty(2 * count, dtype=dt, device="cuda")
+    thff.fill_uniform(T, x, count, seed)
+    y = torch.empty_like(x)
+    z = torch.empty_like(x)
+    thff.ThunderFFTInitialize(T, n)
+    rows = _subset_rows(batch)
+    rows_t = torch.from_numpy(rows).cuda()
+    for forward in directions:
+        thff.ThunderFFT_global(T, n, forward, x, y, batch)
+        sub = from_device(y.view(batch, 2 * n).index_select(0, rows_t).contiguous(), T)
+        sub = sub.reshape(len(rows), n)
+        xin = np.concatenate([oracle.uniform(n, 1, seed, first_element=int(r) * n) for r in rows])
+        ref = oracle.fft(oracle.represent(xin, T), forward)
+        m = oracle.metrics(sub, ref)
+        print(f"{T} N={n} batch={batch} {'fwd' if forward else 'inv'} subset rel_l2="
+              f"{m['rel_l2']:.3e}", flush=True)
+        assert m["nonfinite"] == 0 and m["rel_l2"] <= GATE and m["rel_l2"] <= TIGHT[T]
+        # round trip: inverse of the other direction gives N*x (unnormalized)
+        thff.ThunderFFT_global(T, n, not forward, y, z, batch)
+        xf = x.float()
+        err = torch.linalg.vector_norm(z.float() - n * xf) / torch.linalg.vector_norm(n * xf)
+        rt = float(err)
+        print(f"  round trip rel_l2={rt:.3e}", flush=True)
+        assert np.isfinite(rt) and rt <= GATE and rt <= 2 * TIGHT[T]
+    del x, y, z
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("batch", [65536, 65537])
+def test_config2_n1024_float(batch):
+    """N=1024, batch 65536 (and 65537: masked partial block)."""
+    _large_case("float", 1024, batch)
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("n", SIZES)
+def test_config3_sweep(T, n):
+    """batch = 2^26 / N complex values per buffer."""
+    _large_case(T, n, (1 << 26) // n)

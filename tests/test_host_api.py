@@ -1,0 +1,74 @@
+"""The drop-in boundary on the CPU: library exports, the reference's 18 host API
+checks (sample/validation/fft_validation.cu:320-352) through both the Python
+mirror and the C++ template API, all decided before any HIP call."""
+import os
+import re
+import subprocess
+
+import pytest
+
+import thunderfft_amd as thff
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "thunderfft", "thunderfft.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(thff_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    syms = declared_symbols()
+    assert len(syms) >= 8
+    L = thff.lib()
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, missing
+    assert L.thff_version() >= 100
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+def test_host_checks_python(T):
+    checks = 0
+    for args, what in [((0, 0, -1), "negative batch"), ((0, 8, 1), "null input"),
+                       ((8, 0, 1), "null output"), ((8, 8, 1), "aliased input/output")]:
+        with pytest.raises(ValueError):
+            thff.ThunderFFT_global(T, 64, True, *args)
+        checks += 1
+    thff.ThunderFFT_global(T, 64, True, 0, 0, 0)  # zero batch: no-op before pointers/HIP
+    checks += 1
+    for n in (-1, 0, 32, 8192):
+        with pytest.raises(ValueError, match="unsupported FFT size"):
+            thff.ThunderFFTInitialize(T, n)
+        checks += 1
+    assert checks == 9
+
+
+def test_check_order_and_messages():
+    # the reference checks batch sign before the pointers (thunderfft_impl_kernel.cuh:18-21)
+    with pytest.raises(ValueError, match="nonnegative"):
+        thff.ThunderFFT_global("float", 64, True, 8, 8, -1)
+    with pytest.raises(ValueError, match="Unsupported ThunderFFT length"):
+        thff.ThunderFFT_global("float", 100, True, 8, 16, 1)
+    with pytest.raises(ValueError):
+        thff.ThunderFFT_global("double", 64, True, 8, 16, 1)
+    with pytest.raises(ValueError):
+        thff.ThunderFFTInitialize("bf16", 64)
+    assert thff.transforms_per_block(1024) == 4 and thff.transforms_per_block(64) == 64
+
+
+def test_cpp_template_api_host_only():
+    """Compile the C++ validation program against <thunderfft/thunderfft.cuh> and
+    run its --host-only mode (the reference's GPU-free test, README.md:53)."""
+    exe = os.path.join(ROOT, "thunderfft_amd", "_build", "thff_validate")
+    if not os.path.exists(exe):
+        from thunderfft_amd import build
+        build.build_apps()
+    env = dict(os.environ, HIP_VISIBLE_DEVICES="")
+    res = subprocess.run([exe, "--host-only"], capture_output=True, text=True, env=env,
+                         timeout=120)
+    assert res.returncode == 0, res.stderr
+    assert "18 checks passed before any HIP calls" in res.stderr
+    bad = subprocess.run([exe, "--bogus"], capture_output=True, text=True, env=env, timeout=60)
+    assert bad.returncode == 2

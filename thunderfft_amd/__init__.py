@@ -1,0 +1,171 @@
+"""thunderfft_amd -- MI355X (gfx950) ThunderFFT: batched C2C FFTs, N = 64..4096.
+
+Python mirror of the reference's host API (mcrl/thunderfft,
+include/thunderfft/thunderfft.cuh:55-63,150-154) over the C ABI of
+``libthunderfft_amd.so`` (declared in include/thunderfft/thunderfft.h):
+
+    ThunderFFTInitialize(T, N)                       # T in {"float", "half"}
+    ThunderFFT_global(T, N, forward, d_in, d_out, batch, stream=0)
+    ThunderFFTFinalize(T)
+
+Errors keep the reference's two kinds: ``ValueError`` where the reference
+throws ``std::invalid_argument`` (raised before any HIP call) and
+``RuntimeError("[ThunderFFT] ...")`` where it throws ``std::runtime_error``.
+
+Pointers are plain integers (device addresses); torch tensors are accepted
+and their ``data_ptr()`` is used.  There is no CPU path: importing this module
+fails loudly if the HIP library has not been built.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+__all__ = [
+    "SUPPORTED_N", "PRECISIONS", "lib", "ThunderFFTInitialize", "ThunderFFTFinalize",
+    "ThunderFFT_global", "ThunderFFT_global_async", "twiddle_info", "fill_uniform",
+    "fft", "transforms_per_block", "LIB_PATH",
+]
+
+SUPPORTED_N = (64, 128, 256, 512, 1024, 2048, 4096)
+PRECISIONS = {"float": 0, "half": 1}
+THFF_OK, THFF_EINVAL, THFF_EIO = 0, -22, -5
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libthunderfft_amd.so")
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libthunderfft_amd.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -m thunderfft_amd.build` "
+                "(there is no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        vp = ctypes.c_void_p
+        L.thff_version.restype = ctypes.c_int
+        L.thff_last_error.restype = ctypes.c_char_p
+        L.thff_initialize.argtypes = [ctypes.c_int, ctypes.c_int]
+        L.thff_finalize.argtypes = [ctypes.c_int]
+        sig = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, ctypes.c_int, vp]
+        L.thff_global.argtypes = sig
+        L.thff_global_async.argtypes = sig
+        L.thff_twiddle_info.argtypes = [ctypes.c_int, ctypes.POINTER(vp),
+                                        ctypes.POINTER(ctypes.c_int)]
+        L.thff_fill_uniform.argtypes = [ctypes.c_int, vp, ctypes.c_longlong, ctypes.c_ulonglong,
+                                        ctypes.c_longlong, vp]
+        _lib = L
+    return _lib
+
+
+def _precision(T) -> int:
+    if isinstance(T, str) and T in PRECISIONS:
+        return PRECISIONS[T]
+    name = getattr(T, "__name__", None) or str(T)
+    for key, code in (("float16", 1), ("half", 1), ("complex32", 1), ("float32", 0),
+                      ("float", 0), ("complex64", 0)):
+        if key in name:
+            return code
+    raise ValueError(f"ThunderFFT supports float and half only (got {T!r})")
+
+
+def _ptr(x) -> int:
+    if x is None:
+        return 0
+    if isinstance(x, int):
+        return x
+    if hasattr(x, "data_ptr"):
+        return int(x.data_ptr())
+    raise TypeError(f"expected a device pointer or tensor, got {type(x).__name__}")
+
+
+def _stream(s) -> int:
+    if s is None or s == 0:
+        return 0
+    if isinstance(s, int):
+        return s
+    handle = getattr(s, "cuda_stream", None)
+    if handle is None:
+        raise TypeError("stream must be an integer hipStream_t or a torch.cuda.Stream")
+    return int(handle)
+
+
+def _raise(rc: int) -> None:
+    if rc == THFF_OK:
+        return
+    msg = lib().thff_last_error().decode()
+    if rc == THFF_EINVAL:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def ThunderFFTInitialize(T, N: int) -> None:
+    """ThunderFFTInitialize<T>(N): build this device's twiddle table for (T, N)."""
+    _raise(lib().thff_initialize(_precision(T), int(N)))
+
+
+def ThunderFFTFinalize(T) -> None:
+    """ThunderFFTFinalize<T>(): release this device's twiddle table for T."""
+    _raise(lib().thff_finalize(_precision(T)))
+
+
+def ThunderFFT_global(T, N: int, forward: bool, d_input, d_output, batch: int, stream=0) -> None:
+    """ThunderFFT_global<T,N,forward>(d_input, d_output, batch, stream); synchronous."""
+    _raise(lib().thff_global(_precision(T), int(N), int(bool(forward)), _ptr(d_input),
+                             _ptr(d_output), int(batch), _stream(stream)))
+
+
+def ThunderFFT_global_async(T, N: int, forward: bool, d_input, d_output, batch: int,
+                            stream=0) -> None:
+    """As ThunderFFT_global, but returns once the launch is enqueued on ``stream``."""
+    _raise(lib().thff_global_async(_precision(T), int(N), int(bool(forward)), _ptr(d_input),
+                                   _ptr(d_output), int(batch), _stream(stream)))
+
+
+def twiddle_info(T) -> tuple[int, int]:
+    """(device pointer, N) of this device's twiddle table for T; (0, 0) when released."""
+    p = ctypes.c_void_p()
+    n = ctypes.c_int()
+    _raise(lib().thff_twiddle_info(_precision(T), ctypes.byref(p), ctypes.byref(n)))
+    return int(p.value or 0), int(n.value)
+
+
+def fill_uniform(T, d_out, count: int, seed: int, first_element: int = 0, stream=0) -> None:
+    """Seeded U[-1,1) complex values (same formula as the test oracle's generator)."""
+    _raise(lib().thff_fill_uniform(_precision(T), _ptr(d_out), int(count),
+                                   int(seed) & (2**64 - 1), int(first_element), _stream(stream)))
+
+
+def transforms_per_block(N: int) -> int:
+    """Transforms per 256-lane workgroup of the global kernel."""
+    return 256 * 16 // int(N)
+
+
+def fft(x, forward: bool = True, out=None):
+    """Transform the last axis of a CUDA tensor (complex64 or float16[..., N, 2]).
+
+    A convenience over ThunderFFT_global: initialises the twiddle table for
+    (T, N) on the tensor's device if needed and returns a new tensor.
+    """
+    import torch
+
+    if x.dtype == torch.complex64:
+        T, n = "float", x.shape[-1]
+    elif x.dtype == torch.float16 and x.dim() >= 2 and x.shape[-1] == 2:
+        T, n = "half", x.shape[-2]
+    else:
+        raise ValueError("fft expects complex64 or float16[..., N, 2] tensors")
+    if not x.is_cuda:
+        raise ValueError("fft expects a device tensor (there is no CPU path)")
+    x = x.contiguous()
+    if out is None:
+        out = torch.empty_like(x)
+    batch = x.numel() // (n * (2 if T == "half" else 1))
+    with torch.cuda.device(x.device):
+        if twiddle_info(T)[1] != n:
+            ThunderFFTInitialize(T, n)
+        ThunderFFT_global(T, n, forward, x, out, batch, torch.cuda.current_stream(x.device))
+    return out

@@ -1,0 +1,40 @@
+// c2c_instance.hip -- instantiates the C2C kernels of one length THFF_N
+// (compiled once per length, -DTHFF_N=64 ... 4096, so the lengths build in
+// parallel).
+#include "fft_c2c.hpp"
+#include "launch.hpp"
+
+#ifndef THFF_N
+#error "compile with -DTHFF_N=<transform length>"
+#endif
+
+namespace thff {
+
+template <int N>
+hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, int batch,
+                      const float2* tw, hipStream_t stream) {
+    using P = C2CPlan<N>;
+    const unsigned grid = static_cast<unsigned>((static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB);
+    const dim3 block(P::kWG);
+    if (precision == 0) {
+        const auto* x = static_cast<const float2*>(in);
+        auto* y = static_cast<float2*>(out);
+        if (forward)
+            c2c_kernel<float2, N, true><<<grid, block, 0, stream>>>(x, y, batch, tw);
+        else
+            c2c_kernel<float2, N, false><<<grid, block, 0, stream>>>(x, y, batch, tw);
+    } else {
+        const auto* x = static_cast<const __half2*>(in);
+        auto* y = static_cast<__half2*>(out);
+        if (forward)
+            c2c_kernel<__half2, N, true><<<grid, block, 0, stream>>>(x, y, batch, tw);
+        else
+            c2c_kernel<__half2, N, false><<<grid, block, 0, stream>>>(x, y, batch, tw);
+    }
+    return hipGetLastError();
+}
+
+template hipError_t launch_c2c<THFF_N>(int, bool, const void*, void*, int, const float2*,
+                                       hipStream_t);
+
+}  // namespace thff

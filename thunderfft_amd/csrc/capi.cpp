@@ -1,0 +1,217 @@
+// capi.cpp -- the C ABI of include/thunderfft/thunderfft.h: argument checks,
+// the per-(device, precision) twiddle cache and kernel dispatch.
+//
+// Check order and error kinds follow the reference host wrapper
+// (include/thunderfft/detail/thunderfft_impl_kernel.cuh:13-21) and cache
+// (include/thunderfft/detail/thunderfft_impl_twiddle.cuh:279-327,358-378):
+// invalid arguments are reported before any HIP call, HIP failures as
+// "[ThunderFFT] <context>: <hip error string>".
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+#include <cstdint>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "launch.hpp"
+#include "thunderfft/thunderfft.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& message) {
+    g_last_error = message;
+    return code;
+}
+
+int fail_hip(hipError_t err, const char* context) {
+    return fail(THFF_EIO, std::string("[ThunderFFT] ") + context + ": " + hipGetErrorString(err));
+}
+
+bool supported_length(int n) {
+    return n == 64 || n == 128 || n == 256 || n == 512 || n == 1024 || n == 2048 || n == 4096;
+}
+
+bool supported_precision(int p) { return p == THFF_FLOAT || p == THFF_HALF; }
+
+const char* precision_name(int p) { return p == THFF_FLOAT ? "float" : "half"; }
+
+// One cached table per (device, precision), replaced when N changes
+// (thunderfft_impl_twiddle.cuh:26-36,310-326).
+struct CacheEntry {
+    float2* table = nullptr;
+    int n = 0;
+};
+std::map<int, CacheEntry> g_cache[2];
+std::mutex g_mutex[2];
+
+// W[m] = (cos, sin)(2*pi*m/N) in fp64, rounded once to fp32; the quarter
+// points are exact so that W[0] = 1 + 0i bit for bit.
+std::vector<float2> build_table(int n) {
+    std::vector<float2> h(n);
+    const double tau = 6.283185307179586476925286766559;
+    for (int m = 0; m < n; ++m) {
+        const double a = tau * static_cast<double>(m) / static_cast<double>(n);
+        h[m] = make_float2(static_cast<float>(std::cos(a)), static_cast<float>(std::sin(a)));
+    }
+    h[0] = make_float2(1.f, 0.f);
+    h[n / 4] = make_float2(0.f, 1.f);
+    h[n / 2] = make_float2(-1.f, 0.f);
+    h[3 * n / 4] = make_float2(0.f, -1.f);
+    return h;
+}
+
+hipError_t dispatch(int n, int precision, bool forward, const void* in, void* out, int batch,
+                    const float2* tw, hipStream_t s) {
+    switch (n) {
+    case 64: return thff::launch_c2c<64>(precision, forward, in, out, batch, tw, s);
+    case 128: return thff::launch_c2c<128>(precision, forward, in, out, batch, tw, s);
+    case 256: return thff::launch_c2c<256>(precision, forward, in, out, batch, tw, s);
+    case 512: return thff::launch_c2c<512>(precision, forward, in, out, batch, tw, s);
+    case 1024: return thff::launch_c2c<1024>(precision, forward, in, out, batch, tw, s);
+    case 2048: return thff::launch_c2c<2048>(precision, forward, in, out, batch, tw, s);
+    case 4096: return thff::launch_c2c<4096>(precision, forward, in, out, batch, tw, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+int global_impl(int precision, int n, int forward, const void* d_input, void* d_output, int batch,
+                void* stream, bool synchronize) {
+    if (!supported_precision(precision))
+        return fail(THFF_EINVAL, "ThunderFFT_global supports float and half only");
+    if (!supported_length(n)) return fail(THFF_EINVAL, "Unsupported ThunderFFT length");
+    if (batch < 0) return fail(THFF_EINVAL, "ThunderFFT batch must be nonnegative");
+    if (batch == 0) return THFF_OK;
+    if (!d_input || !d_output || d_input == d_output)
+        return fail(THFF_EINVAL, "ThunderFFT requires separate non-null input/output buffers");
+    // The dispatch grid counts work-items in 32 bits.
+    const long long fpb = thff::c2c_transforms_per_block(n);
+    const long long items = (static_cast<long long>(batch) + fpb - 1) / fpb * 256;
+    if (items > static_cast<long long>(UINT32_MAX))
+        return fail(THFF_EINVAL, "ThunderFFT batch exceeds one launch for this length");
+
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return fail_hip(err, "hipGetDevice (ThunderFFT_global)");
+    const float2* table = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_mutex[precision]);
+        const auto found = g_cache[precision].find(device);
+        if (found != g_cache[precision].end() && found->second.n == n) table = found->second.table;
+    }
+    if (!table)
+        return fail(THFF_EIO, std::string("[ThunderFFT] ThunderFFT_global: no twiddle table for N=") +
+                                  std::to_string(n) + " on device " + std::to_string(device) +
+                                  "; call ThunderFFTInitialize<" + precision_name(precision) +
+                                  ">(" + std::to_string(n) + ") first");
+    auto s = static_cast<hipStream_t>(stream);
+    err = dispatch(n, precision, forward != 0, d_input, d_output, batch, table, s);
+    if (err != hipSuccess) return fail_hip(err, "ThunderFFT_global launch");
+    if (synchronize) {
+        err = hipStreamSynchronize(s);
+        if (err != hipSuccess) return fail_hip(err, "ThunderFFT_global synchronize");
+    }
+    return THFF_OK;
+}
+
+}  // namespace
+
+namespace thff {
+int c2c_transforms_per_block(int n) { return 256 * 16 / n; }
+}  // namespace thff
+
+extern "C" {
+
+int thff_version(void) { return 100; }
+
+const char* thff_last_error(void) { return g_last_error.c_str(); }
+
+int thff_initialize(int precision, int n) {
+    if (!supported_precision(precision))
+        return fail(THFF_EINVAL, "ThunderFFTInitialize<T>: supported T are float and half only");
+    if (!supported_length(n))
+        return fail(THFF_EINVAL, "ThunderFFTInitialize<T>: unsupported FFT size");
+    std::lock_guard<std::mutex> lock(g_mutex[precision]);
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return fail_hip(err, "hipGetDevice (initialize)");
+    CacheEntry& entry = g_cache[precision][device];
+    if (entry.table && entry.n == n) return THFF_OK;
+    if (entry.table) {
+        entry.n = 0;
+        err = hipFree(entry.table);
+        entry.table = nullptr;
+        if (err != hipSuccess) return fail_hip(err, "hipFree cached twiddle (initialize)");
+    }
+    const std::vector<float2> host = build_table(n);
+    float2* table = nullptr;
+    err = hipMalloc(reinterpret_cast<void**>(&table), sizeof(float2) * n);
+    if (err != hipSuccess) return fail_hip(err, "hipMalloc twiddle table");
+    err = hipMemcpy(table, host.data(), sizeof(float2) * n, hipMemcpyHostToDevice);
+    if (err != hipSuccess) {
+        (void)hipFree(table);
+        return fail_hip(err, "hipMemcpy twiddle table");
+    }
+    entry.table = table;
+    entry.n = n;
+    return THFF_OK;
+}
+
+int thff_finalize(int precision) {
+    if (!supported_precision(precision))
+        return fail(THFF_EINVAL, "ThunderFFTFinalize<T>: supported T are float and half only");
+    std::lock_guard<std::mutex> lock(g_mutex[precision]);
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return fail_hip(err, "hipGetDevice (finalize)");
+    const auto found = g_cache[precision].find(device);
+    if (found == g_cache[precision].end()) return THFF_OK;
+    float2* table = found->second.table;
+    g_cache[precision].erase(found);
+    if (table) {
+        err = hipFree(table);
+        if (err != hipSuccess) return fail_hip(err, "hipFree cached twiddle (finalize)");
+    }
+    return THFF_OK;
+}
+
+int thff_global(int precision, int n, int forward, const void* d_input, void* d_output, int batch,
+                void* stream) {
+    return global_impl(precision, n, forward, d_input, d_output, batch, stream, true);
+}
+
+int thff_global_async(int precision, int n, int forward, const void* d_input, void* d_output,
+                      int batch, void* stream) {
+    return global_impl(precision, n, forward, d_input, d_output, batch, stream, false);
+}
+
+int thff_twiddle_info(int precision, const void** d_table, int* n) {
+    if (!supported_precision(precision)) return fail(THFF_EINVAL, "unsupported precision");
+    if (!d_table || !n) return fail(THFF_EINVAL, "thff_twiddle_info: null output pointer");
+    std::lock_guard<std::mutex> lock(g_mutex[precision]);
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return fail_hip(err, "hipGetDevice (twiddle info)");
+    const auto found = g_cache[precision].find(device);
+    *d_table = found == g_cache[precision].end() ? nullptr : found->second.table;
+    *n = found == g_cache[precision].end() ? 0 : found->second.n;
+    return THFF_OK;
+}
+
+int thff_fill_uniform(int precision, void* d_out, long long count, unsigned long long seed,
+                      long long first_element, void* stream) {
+    if (!supported_precision(precision)) return fail(THFF_EINVAL, "unsupported precision");
+    if (count < 0 || first_element < 0) return fail(THFF_EINVAL, "negative count or offset");
+    if (count == 0) return THFF_OK;
+    if (!d_out) return fail(THFF_EINVAL, "thff_fill_uniform: null output");
+    const hipError_t err = thff::launch_fill_uniform(precision, d_out, count, seed, first_element,
+                                                     static_cast<hipStream_t>(stream));
+    if (err != hipSuccess) return fail_hip(err, "thff_fill_uniform launch");
+    return THFF_OK;
+}
+
+}  // extern "C"
