@@ -12,29 +12,31 @@ namespace thff {
 
 template <int N>
 hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, int batch,
-                      const float2* tw, hipStream_t stream) {
+                      const float2* tw, int num_cus, hipStream_t stream) {
     using P = C2CPlan<N>;
-    const unsigned grid = static_cast<unsigned>((static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB);
+    const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
+    const int tpb = c2c_tiles_per_block(ntiles, num_cus);
+    const unsigned grid = static_cast<unsigned>((ntiles + tpb - 1) / tpb);
     const dim3 block(P::kWG);
     if (precision == 0) {
         const auto* x = static_cast<const float2*>(in);
         auto* y = static_cast<float2*>(out);
         if (forward)
-            c2c_kernel<float2, N, true><<<grid, block, 0, stream>>>(x, y, batch, tw);
+            c2c_kernel<float2, N, true><<<grid, block, 0, stream>>>(x, y, batch, tw, tpb);
         else
-            c2c_kernel<float2, N, false><<<grid, block, 0, stream>>>(x, y, batch, tw);
+            c2c_kernel<float2, N, false><<<grid, block, 0, stream>>>(x, y, batch, tw, tpb);
     } else {
         const auto* x = static_cast<const __half2*>(in);
         auto* y = static_cast<__half2*>(out);
         if (forward)
-            c2c_kernel<__half2, N, true><<<grid, block, 0, stream>>>(x, y, batch, tw);
+            c2c_kernel<__half2, N, true><<<grid, block, 0, stream>>>(x, y, batch, tw, tpb);
         else
-            c2c_kernel<__half2, N, false><<<grid, block, 0, stream>>>(x, y, batch, tw);
+            c2c_kernel<__half2, N, false><<<grid, block, 0, stream>>>(x, y, batch, tw, tpb);
     }
     return hipGetLastError();
 }
 
-template hipError_t launch_c2c<THFF_N>(int, bool, const void*, void*, int, const float2*,
+template hipError_t launch_c2c<THFF_N>(int, bool, const void*, void*, int, const float2*, int,
                                        hipStream_t);
 
 }  // namespace thff

@@ -45,6 +45,7 @@ const char* precision_name(int p) { return p == THFF_FLOAT ? "float" : "half"; }
 struct CacheEntry {
     float2* table = nullptr;
     int n = 0;
+    int num_cus = 0;
 };
 std::map<int, CacheEntry> g_cache[2];
 std::mutex g_mutex[2];
@@ -66,15 +67,15 @@ std::vector<float2> build_table(int n) {
 }
 
 hipError_t dispatch(int n, int precision, bool forward, const void* in, void* out, int batch,
-                    const float2* tw, hipStream_t s) {
+                    const float2* tw, int cus, hipStream_t s) {
     switch (n) {
-    case 64: return thff::launch_c2c<64>(precision, forward, in, out, batch, tw, s);
-    case 128: return thff::launch_c2c<128>(precision, forward, in, out, batch, tw, s);
-    case 256: return thff::launch_c2c<256>(precision, forward, in, out, batch, tw, s);
-    case 512: return thff::launch_c2c<512>(precision, forward, in, out, batch, tw, s);
-    case 1024: return thff::launch_c2c<1024>(precision, forward, in, out, batch, tw, s);
-    case 2048: return thff::launch_c2c<2048>(precision, forward, in, out, batch, tw, s);
-    case 4096: return thff::launch_c2c<4096>(precision, forward, in, out, batch, tw, s);
+    case 64: return thff::launch_c2c<64>(precision, forward, in, out, batch, tw, cus, s);
+    case 128: return thff::launch_c2c<128>(precision, forward, in, out, batch, tw, cus, s);
+    case 256: return thff::launch_c2c<256>(precision, forward, in, out, batch, tw, cus, s);
+    case 512: return thff::launch_c2c<512>(precision, forward, in, out, batch, tw, cus, s);
+    case 1024: return thff::launch_c2c<1024>(precision, forward, in, out, batch, tw, cus, s);
+    case 2048: return thff::launch_c2c<2048>(precision, forward, in, out, batch, tw, cus, s);
+    case 4096: return thff::launch_c2c<4096>(precision, forward, in, out, batch, tw, cus, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -98,10 +99,14 @@ int global_impl(int precision, int n, int forward, const void* d_input, void* d_
     hipError_t err = hipGetDevice(&device);
     if (err != hipSuccess) return fail_hip(err, "hipGetDevice (ThunderFFT_global)");
     const float2* table = nullptr;
+    int cus = 0;
     {
         std::lock_guard<std::mutex> lock(g_mutex[precision]);
         const auto found = g_cache[precision].find(device);
-        if (found != g_cache[precision].end() && found->second.n == n) table = found->second.table;
+        if (found != g_cache[precision].end() && found->second.n == n) {
+            table = found->second.table;
+            cus = found->second.num_cus;
+        }
     }
     if (!table)
         return fail(THFF_EIO, std::string("[ThunderFFT] ThunderFFT_global: no twiddle table for N=") +
@@ -109,7 +114,7 @@ int global_impl(int precision, int n, int forward, const void* d_input, void* d_
                                   "; call ThunderFFTInitialize<" + precision_name(precision) +
                                   ">(" + std::to_string(n) + ") first");
     auto s = static_cast<hipStream_t>(stream);
-    err = dispatch(n, precision, forward != 0, d_input, d_output, batch, table, s);
+    err = dispatch(n, precision, forward != 0, d_input, d_output, batch, table, cus, s);
     if (err != hipSuccess) return fail_hip(err, "ThunderFFT_global launch");
     if (synchronize) {
         err = hipStreamSynchronize(s);
@@ -147,6 +152,9 @@ int thff_initialize(int precision, int n) {
         entry.table = nullptr;
         if (err != hipSuccess) return fail_hip(err, "hipFree cached twiddle (initialize)");
     }
+    int cus = 0;
+    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (err != hipSuccess) return fail_hip(err, "hipDeviceGetAttribute (initialize)");
     const std::vector<float2> host = build_table(n);
     float2* table = nullptr;
     err = hipMalloc(reinterpret_cast<void**>(&table), sizeof(float2) * n);
@@ -158,6 +166,7 @@ int thff_initialize(int precision, int n) {
     }
     entry.table = table;
     entry.n = n;
+    entry.num_cus = cus;
     return THFF_OK;
 }
 

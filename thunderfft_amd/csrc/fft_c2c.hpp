@@ -2,17 +2,31 @@
 //
 // Replaces detail::ThunderFFT_global_kernel<T,N,fwd> of the reference
 // (include/thunderfft/detail/kernel/global_kernel.cuh:21-100): natural-order
-// signals of N complex values at in[b*N], out[b*N]; the last workgroup may
-// hold fewer than FPB valid transforms, whose inputs are never read and whose
-// outputs are never written.
+// signals of N complex values at in[b*N], out[b*N]; the last tile may hold
+// fewer than kFPB valid transforms, whose inputs are never read (they are
+// zero-filled) and whose outputs are never written.
 //
-// Layout per workgroup (256 lanes = 4 wave64s): every transform is owned by
-// TPF = N/16 lanes holding 16 complex values each.  N <= 1024: each wave owns
-// 1024/N whole transforms and a private LDS region, synchronised at wave
-// scope; the wave's 1024 contiguous input values are staged through LDS with
-// 16-byte loads when N < 1024, so global traffic stays fully coalesced.
-// N = 2048/4096: a transform spans 2/4 waves and passes synchronise the
-// workgroup.  LDS holds fp32 complex values padded by one slot every 16.
+// Work decomposition.  A workgroup is 256 lanes (4 wave64s) and processes
+// "tiles" of 4096 complex values (4096/N whole transforms), 16 values per
+// lane.  Every transform is owned by TPF = N/16 lanes.  A workgroup walks
+// `tiles_per_block` consecutive tiles and prefetches the next tile's input
+// into registers before it transforms the current one, so every wave keeps
+// a full tile of HBM reads in flight while it computes.
+//
+//   N <= 1024: each wave owns 1024/N whole transforms and a private LDS
+//              region, synchronised at wave scope.  For N < 1024 the wave's
+//              1024 contiguous input values are read with 16-byte loads and
+//              redistributed through LDS (and the same on the way out), so
+//              global traffic is fully coalesced.
+//   N >= 2048: a transform spans 2 or 4 waves and passes synchronise the
+//              workgroup.
+//
+// Twiddles W_{LR}^{j*k} of every Stockham pass depend only on the lane, so
+// each lane computes its (at most 30) factors once from the device table
+// and keeps them in registers for all the tiles it processes.
+//
+// Global loads and stores are non-temporal: every byte is touched exactly
+// once, so the data should not displace anything in the caches.
 #pragma once
 
 #include "fft_core.hpp"
@@ -25,16 +39,20 @@ struct C2CPlan {
                       N == 4096,
                   "unsupported transform length");
     static constexpr int kE = 16;                 // complex values per lane
-    static constexpr int kTPF = N / kE;           // lanes per transform
     static constexpr int kWG = 256;               // lanes per workgroup
-    static constexpr int kFPB = kWG / kTPF;       // transforms per workgroup
+    static constexpr int kTile = kWG * kE;        // complex values per tile
+    static constexpr int kTPF = N / kE;           // lanes per transform
+    static constexpr int kFPB = kTile / N;        // transforms per tile
     static constexpr int kR0 = 16;
     static constexpr int kR1 = N == 64 ? 4 : N == 128 ? 8 : 16;
     static constexpr int kR2 = N / (kR0 * kR1);   // 1 when two passes suffice
+    static constexpr int kRLast = kR2 > 1 ? kR2 : kR1;
     static constexpr bool kWaveLocal = kTPF <= 64;
     static constexpr bool kStaged = kTPF < 64;
     static constexpr int kSlot = N + N / 16;      // padded LDS slots per transform
     static constexpr int kLdsSlots = kFPB * kSlot;
+    static constexpr int kTw1 = (16 / kR1) * (kR1 - 1);                  // pass-1 factors per lane
+    static constexpr int kTw2 = kR2 > 1 ? (16 / kR2) * (kR2 - 1) : 0;   // pass-2 factors per lane
 };
 
 __device__ __forceinline__ int lds_pad(int i) { return i + (i >> 4); }
@@ -47,20 +65,29 @@ __device__ __forceinline__ void region_sync() {
         __syncthreads();
 }
 
-// Twiddle W_{LR}^{e'} for the pass, read from the fp32 table tw[m] =
-// (cos, sin)(2*pi*m/N) (positive angle, as the reference's table
-// thunderfft_impl_twiddle.cuh:76-91) and conjugated for the forward direction.
-template <int N, bool FWD>
-__device__ __forceinline__ cpx apply_twiddle(cpx v, const float2* __restrict__ tw, int e) {
-    const float2 w = tw[e & (N - 1)];
-    return FWD ? cmulc(v, cpx{w.x, w.y}) : cmul(v, cpx{w.x, w.y});
+// Per-lane twiddles of the pass of radix R that follows sub-transforms of
+// length L: for butterfly b = t + TPF*q (q < 16/R) and input j (1 <= j < R),
+// W_{LR}^{j*(b mod L)}, read from the fp32 table tw[m] = (cos, sin)(2*pi*m/N)
+// (positive angle, as the reference's table, thunderfft_impl_twiddle.cuh:
+// 76-91) and conjugated once here for the forward direction.
+template <int N, bool FWD, int R, int L>
+__device__ __forceinline__ void pass_twiddles(cpx* w, int t, const float2* __restrict__ tw) {
+    using P = C2CPlan<N>;
+#pragma unroll
+    for (int q = 0; q < 16 / R; ++q) {
+        const int k = (t + P::kTPF * q) % L;
+#pragma unroll
+        for (int j = 1; j < R; ++j) {
+            const float2 x = tw[(j * k * (N / (L * R))) & (N - 1)];
+            w[q * (R - 1) + j - 1] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+        }
+    }
 }
 
 // One Stockham pass p >= 1: write the previous pass's outputs to LDS, read
 // this pass's inputs, twiddle, DFT.
 template <int N, bool FWD, int R, int L, int RPrev, int LPrev>
-__device__ __forceinline__ void stockham_pass(cpx (&v)[16], cpx* slot, int t,
-                                              const float2* __restrict__ tw) {
+__device__ __forceinline__ void stockham_pass(cpx (&v)[16], cpx* slot, int t, const cpx* w) {
     using P = C2CPlan<N>;
     // previous outputs: butterfly b = t + TPF*q, output m -> (b/LPrev)*LPrev*RPrev + b%LPrev + m*LPrev
     region_sync<P::kWaveLocal>();
@@ -75,106 +102,146 @@ __device__ __forceinline__ void stockham_pass(cpx (&v)[16], cpx* slot, int t,
 #pragma unroll
     for (int q = 0; q < 16 / R; ++q) {
         const int b = t + P::kTPF * q;
-        const int k = b % L;
 #pragma unroll
         for (int j = 0; j < R; ++j) {
-            cpx x = slot[lds_pad(b + j * (N / R))];
-            if (j > 0) x = apply_twiddle<N, FWD>(x, tw, j * k * (N / (L * R)));
-            v[q * R + j] = x;
+            const cpx x = slot[lds_pad(b + j * (N / R))];
+            v[q * R + j] = j == 0 ? x : cmul(x, w[q * (R - 1) + j - 1]);
         }
         Dft<R, FWD>::run(v + q * R);
     }
 }
 
+// Raw per-lane input of one tile, as loaded from global memory.
+//   staged:     16/kVec 16-byte vectors of kVec consecutive values each;
+//   not staged: 16 single values (8 or 4 bytes).
+template <class IO, int N>
+struct TileRaw {
+    using P = C2CPlan<N>;
+    using W = std::conditional_t<P::kStaged, typename Io<IO>::W4, typename Io<IO>::W1>;
+    static constexpr int kCount = P::kStaged ? 16 / Io<IO>::kVec : 16;
+    W w[kCount];
+};
+
 template <class IO, int N, bool FWD>
 __global__ __launch_bounds__(256) void c2c_kernel(const IO* __restrict__ in, IO* __restrict__ out,
-                                                  int batch, const float2* __restrict__ tw) {
+                                                  int batch, const float2* __restrict__ tw,
+                                                  int tiles_per_block) {
     using P = C2CPlan<N>;
+    using I = Io<IO>;
+    using Raw = TileRaw<IO, N>;
     __shared__ cpx lds[P::kLdsSlots];
     const int tid = threadIdx.x;
-    const int f = tid / P::kTPF;  // transform slot within the workgroup
+    const int f = tid / P::kTPF;  // transform slot within the tile
     const int t = tid % P::kTPF;  // lane within the transform
-    const long long first = static_cast<long long>(blockIdx.x) * P::kFPB;
+    const int wave = tid >> 6, lane = tid & 63;
+    constexpr int kFPW = P::kStaged ? 64 / P::kTPF : 1;  // transforms per wave (staged)
+    constexpr int kVec = I::kVec;
     cpx* slot = lds + f * P::kSlot;
-    cpx v[16];
+    cpx* chunk = lds + wave * kFPW * P::kSlot;  // staged: the wave's 1024 values
 
-    // ---- load pass-0 inputs: x[t + j*TPF], j < 16 ----
-    if constexpr (P::kStaged) {
-        constexpr int kFPW = 64 / P::kTPF;  // transforms per wave
-        constexpr int kVec = Io<IO>::kVec;
-        const int wave = tid >> 6, lane = tid & 63;
-        const long long wfirst = first + wave * kFPW;
-        const long long left = static_cast<long long>(batch) - wfirst;
-        const int valid = left <= 0 ? 0 : (left >= kFPW ? 1024 : static_cast<int>(left) * N);
-        cpx* chunk = lds + wave * kFPW * P::kSlot;
-        const IO* src = in + wfirst * N;
+    cpx w1[P::kTw1];
+    cpx w2[P::kTw2 > 0 ? P::kTw2 : 1];
+    pass_twiddles<N, FWD, P::kR1, 16>(w1, t, tw);
+    if constexpr (P::kR2 > 1) pass_twiddles<N, FWD, P::kR2, 16 * P::kR1>(w2, t, tw);
+
+    const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
+    long long tile = static_cast<long long>(blockIdx.x) * tiles_per_block;
+    const long long tile_end = tile + tiles_per_block < ntiles ? tile + tiles_per_block : ntiles;
+    if (tile >= tile_end) return;  // uniform over the workgroup
+
+    // Number of valid values in this wave's staged chunk (0..1024), and
+    // whether this lane's transform exists (not staged).
+    auto staged_valid = [&](long long tl) {
+        const long long left = static_cast<long long>(batch) - (tl * P::kFPB + wave * kFPW);
+        return left <= 0 ? 0 : (left >= kFPW ? 1024 : static_cast<int>(left) * N);
+    };
+    auto load_tile = [&](Raw& r, long long tl) {
+        if constexpr (P::kStaged) {
+            const int valid = staged_valid(tl);
+            const IO* src = in + (tl * P::kFPB + wave * kFPW) * N;
 #pragma unroll
-        for (int i = 0; i < 1024 / (64 * kVec); ++i) {
-            const int e = kVec * lane + 64 * kVec * i;
-            cpx q[kVec];
-            if (e < valid) {
-                Io<IO>::load_vec(src + e, q);
-            } else {
-#pragma unroll
-                for (int c = 0; c < kVec; ++c) q[c] = {0.f, 0.f};
+            for (int i = 0; i < Raw::kCount; ++i) {
+                const int e = kVec * lane + 64 * kVec * i;
+                r.w[i] = e < valid ? ld_nt(reinterpret_cast<const typename Raw::W*>(src + e))
+                                   : typename Raw::W{};
             }
+        } else {
+            const bool active = tl * P::kFPB + f < batch;
+            const IO* src = in + (tl * P::kFPB + f) * N + t;
 #pragma unroll
-            for (int c = 0; c < kVec; ++c) chunk[lds_pad(e + c)] = q[c];
+            for (int j = 0; j < 16; ++j)
+                r.w[j] = active ? ld_nt(reinterpret_cast<const typename Raw::W*>(src + j * P::kTPF))
+                                : typename Raw::W{};
         }
-        wave_lds_sync();
-#pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = slot[lds_pad(t + j * P::kTPF)];
-    } else {
-        const bool active = first + f < batch;
-        const IO* src = in + (first + f) * N;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = active ? Io<IO>::load(src + t + j * P::kTPF) : cpx{0.f, 0.f};
-    }
+    };
 
-    // ---- pass 0: radix 16 over stride-TPF inputs (L = 1, no twiddle) ----
-    Dft<16, FWD>::run(v);
-    // ---- pass 1 ----
-    stockham_pass<N, FWD, P::kR1, 16, 16, 1>(v, slot, t, tw);
-    constexpr int kRLast = P::kR2 > 1 ? P::kR2 : P::kR1;
-    // ---- pass 2 ----
-    if constexpr (P::kR2 > 1) stockham_pass<N, FWD, P::kR2, 16 * P::kR1, P::kR1, 16>(v, slot, t, tw);
+    Raw next;
+    load_tile(next, tile);
+    for (; tile < tile_end; ++tile) {
+        const Raw cur = next;
+        if (tile + 1 < tile_end) load_tile(next, tile + 1);
 
-    // ---- store: last pass output m of butterfly b = t + TPF*q is y[b + m*N/RLast] ----
-    if constexpr (P::kStaged) {
-        region_sync<true>();
+        // ---- pass-0 inputs x[t + j*TPF], j < 16 ----
+        cpx v[16];
+        if constexpr (P::kStaged) {
+            wave_lds_sync();  // the previous tile's reads of this region are done
 #pragma unroll
-        for (int q = 0; q < 16 / kRLast; ++q) {
-            const int b = t + P::kTPF * q;
-#pragma unroll
-            for (int m = 0; m < kRLast; ++m) slot[lds_pad(b + m * (N / kRLast))] = v[q * kRLast + m];
-        }
-        wave_lds_sync();
-        constexpr int kFPW = 64 / P::kTPF;
-        constexpr int kVec = Io<IO>::kVec;
-        const int wave = tid >> 6, lane = tid & 63;
-        const long long wfirst = first + wave * kFPW;
-        const long long left = static_cast<long long>(batch) - wfirst;
-        const int valid = left <= 0 ? 0 : (left >= kFPW ? 1024 : static_cast<int>(left) * N);
-        const cpx* chunk = lds + wave * kFPW * P::kSlot;
-        IO* dst = out + wfirst * N;
-#pragma unroll
-        for (int i = 0; i < 1024 / (64 * kVec); ++i) {
-            const int e = kVec * lane + 64 * kVec * i;
-            if (e < valid) {
+            for (int i = 0; i < Raw::kCount; ++i) {
+                const int e = kVec * lane + 64 * kVec * i;
                 cpx q[kVec];
+                I::decode4(cur.w[i], q);
 #pragma unroll
-                for (int c = 0; c < kVec; ++c) q[c] = chunk[lds_pad(e + c)];
-                Io<IO>::store_vec(dst + e, q);
+                for (int c = 0; c < kVec; ++c) chunk[lds_pad(e + c)] = q[c];
             }
-        }
-    } else {
-        if (first + f < batch) {
-            IO* dst = out + (first + f) * N;
+            wave_lds_sync();
 #pragma unroll
-            for (int q = 0; q < 16 / kRLast; ++q) {
+            for (int j = 0; j < 16; ++j) v[j] = slot[lds_pad(t + j * P::kTPF)];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = I::decode1(cur.w[j]);
+        }
+
+        // ---- pass 0: radix 16 over stride-TPF inputs (L = 1, no twiddle) ----
+        Dft<16, FWD>::run(v);
+        // ---- pass 1 ----
+        stockham_pass<N, FWD, P::kR1, 16, 16, 1>(v, slot, t, w1);
+        // ---- pass 2 ----
+        if constexpr (P::kR2 > 1) stockham_pass<N, FWD, P::kR2, 16 * P::kR1, P::kR1, 16>(v, slot, t, w2);
+
+        // ---- store: last pass output m of butterfly b = t + TPF*q is y[b + m*N/RLast] ----
+        constexpr int kRL = P::kRLast;
+        if constexpr (P::kStaged) {
+            wave_lds_sync();
+#pragma unroll
+            for (int q = 0; q < 16 / kRL; ++q) {
                 const int b = t + P::kTPF * q;
 #pragma unroll
-                for (int m = 0; m < kRLast; ++m) Io<IO>::store(dst + b + m * (N / kRLast), v[q * kRLast + m]);
+                for (int m = 0; m < kRL; ++m) slot[lds_pad(b + m * (N / kRL))] = v[q * kRL + m];
+            }
+            wave_lds_sync();
+            const int valid = staged_valid(tile);
+            IO* dst = out + (tile * P::kFPB + wave * kFPW) * N;
+#pragma unroll
+            for (int i = 0; i < Raw::kCount; ++i) {
+                const int e = kVec * lane + 64 * kVec * i;
+                if (e < valid) {
+                    cpx q[kVec];
+#pragma unroll
+                    for (int c = 0; c < kVec; ++c) q[c] = chunk[lds_pad(e + c)];
+                    st_nt(reinterpret_cast<typename Raw::W*>(dst + e), I::encode4(q));
+                }
+            }
+        } else {
+            if (tile * P::kFPB + f < batch) {
+                IO* dst = out + (tile * P::kFPB + f) * N;
+#pragma unroll
+                for (int q = 0; q < 16 / kRL; ++q) {
+                    const int b = t + P::kTPF * q;
+#pragma unroll
+                    for (int m = 0; m < kRL; ++m)
+                        st_nt(reinterpret_cast<typename Raw::W*>(dst + b + m * (N / kRL)),
+                              I::encode1(v[q * kRL + m]));
+                }
             }
         }
     }

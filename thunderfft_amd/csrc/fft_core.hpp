@@ -142,48 +142,68 @@ struct Dft<4, FWD> {
 // Storage types.  float2 holds (re, im); __half2 holds low = re, high = im
 // (the reference's vec2_t<half>, include/thunderfft/detail/util_cuda.h:46-49).
 // ---------------------------------------------------------------------------
+using u32x2 = unsigned __attribute__((ext_vector_type(2)));
+using u32x4 = unsigned __attribute__((ext_vector_type(4)));
+
+// Non-temporal global accesses (streamed data, touched once).
+template <class W>
+__device__ __forceinline__ W ld_nt(const W* p) {
+    return __builtin_nontemporal_load(p);
+}
+template <class W>
+__device__ __forceinline__ void st_nt(W* p, W w) {
+    __builtin_nontemporal_store(w, p);
+}
+
+// Bit casts taken on plain scalars: clang mis-evaluates __builtin_bit_cast
+// applied directly to an ext-vector element (w.y read as w.x), so elements
+// are always passed by value first.
+__device__ __forceinline__ float as_f32(unsigned u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ unsigned as_u32(float f) { return __builtin_bit_cast(unsigned, f); }
+
 template <class IO>
 struct Io;
 
+// W1 holds one complex value, W4 one 16-byte vector of kVec values.
 template <>
 struct Io<float2> {
-    static constexpr int kVec = 2;  // complex values per 16-byte access
-    __device__ __forceinline__ static cpx load(const float2* p) {
-        const float2 v = *p;
-        return {v.x, v.y};
+    static constexpr int kVec = 2;
+    using W1 = u32x2;
+    using W4 = u32x4;
+    __device__ __forceinline__ static cpx decode1(W1 w) { return {as_f32(w.x), as_f32(w.y)}; }
+    __device__ __forceinline__ static W1 encode1(cpx v) { return W1{as_u32(v.re), as_u32(v.im)}; }
+    __device__ __forceinline__ static void decode4(W4 w, cpx* v) {
+        v[0] = {as_f32(w.x), as_f32(w.y)};
+        v[1] = {as_f32(w.z), as_f32(w.w)};
     }
-    __device__ __forceinline__ static void store(float2* p, cpx v) { *p = make_float2(v.re, v.im); }
-    __device__ __forceinline__ static void load_vec(const float2* p, cpx* v) {
-        const float4 q = *reinterpret_cast<const float4*>(p);
-        v[0] = {q.x, q.y};
-        v[1] = {q.z, q.w};
-    }
-    __device__ __forceinline__ static void store_vec(float2* p, const cpx* v) {
-        *reinterpret_cast<float4*>(p) = make_float4(v[0].re, v[0].im, v[1].re, v[1].im);
+    __device__ __forceinline__ static W4 encode4(const cpx* v) {
+        return W4{as_u32(v[0].re), as_u32(v[0].im), as_u32(v[1].re), as_u32(v[1].im)};
     }
 };
 
 template <>
 struct Io<__half2> {
     static constexpr int kVec = 4;
-    __device__ __forceinline__ static cpx unpack(__half2 h) {
-        const float2 f = __half22float2(h);
+    using W1 = unsigned;
+    using W4 = u32x4;
+    __device__ __forceinline__ static cpx unpack(unsigned w) {
+        const float2 f = __half22float2(__builtin_bit_cast(__half2, w));
         return {f.x, f.y};
     }
-    __device__ __forceinline__ static __half2 pack(cpx v) { return __floats2half2_rn(v.re, v.im); }
-    __device__ __forceinline__ static cpx load(const __half2* p) { return unpack(*p); }
-    __device__ __forceinline__ static void store(__half2* p, cpx v) { *p = pack(v); }
-    __device__ __forceinline__ static void load_vec(const __half2* p, cpx* v) {
-        const uint4 q = *reinterpret_cast<const uint4*>(p);
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = unpack(__builtin_bit_cast(__half2, w[i]));
+    // Round to nearest even, low half = real.
+    __device__ __forceinline__ static unsigned pack(cpx v) {
+        return __builtin_bit_cast(unsigned, __floats2half2_rn(v.re, v.im));
     }
-    __device__ __forceinline__ static void store_vec(__half2* p, const cpx* v) {
-        uint32_t w[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = __builtin_bit_cast(uint32_t, pack(v[i]));
-        *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+    __device__ __forceinline__ static cpx decode1(W1 w) { return unpack(w); }
+    __device__ __forceinline__ static W1 encode1(cpx v) { return pack(v); }
+    __device__ __forceinline__ static void decode4(W4 w, cpx* v) {
+        v[0] = unpack(w.x);
+        v[1] = unpack(w.y);
+        v[2] = unpack(w.z);
+        v[3] = unpack(w.w);
+    }
+    __device__ __forceinline__ static W4 encode4(const cpx* v) {
+        return W4{pack(v[0]), pack(v[1]), pack(v[2]), pack(v[3])};
     }
 };
 

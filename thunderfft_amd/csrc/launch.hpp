@@ -7,13 +7,24 @@
 namespace thff {
 
 // Enqueue the batched C2C kernel for length N.  precision: 0 float2, 1 half2.
-// tw: the device's fp32 table of N values (cos, sin)(2*pi*m/N).
+// tw: the device's fp32 table of N values (cos, sin)(2*pi*m/N); num_cus: the
+// device's compute-unit count (sizes the grid).
 template <int N>
 hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, int batch,
-                      const float2* tw, hipStream_t stream);
+                      const float2* tw, int num_cus, hipStream_t stream);
 
-// Transforms per workgroup (256 lanes) for length N; sizes the grid.
+// Transforms per tile (4096 complex values, one workgroup pass) for length N.
 int c2c_transforms_per_block(int n);
+
+// Tiles each workgroup walks: enough workgroups for about eight per compute
+// unit, at most 16 tiles each, so the hardware dispatcher balances the tail.
+inline int c2c_tiles_per_block(long long ntiles, int num_cus) {
+    const long long target = static_cast<long long>(num_cus > 0 ? num_cus : 256) * 8;
+    long long tpb = ntiles / target;
+    if (tpb < 1) tpb = 1;
+    if (tpb > 16) tpb = 16;
+    return static_cast<int>(tpb);
+}
 
 hipError_t launch_fill_uniform(int precision, void* out, long long count, unsigned long long seed,
                                long long first_element, hipStream_t stream);
