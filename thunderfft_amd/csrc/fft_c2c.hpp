@@ -7,19 +7,19 @@
 // zero-filled) and whose outputs are never written.
 //
 // Work decomposition.  A workgroup is 256 lanes (4 wave64s) and processes
-// "tiles" of 4096 complex values (4096/N whole transforms), 16 values per
-// lane.  Every transform is owned by TPF = N/16 lanes.  A workgroup walks
-// `tiles_per_block` consecutive tiles and prefetches the next tile's input
-// into registers before it transforms the current one, so every wave keeps
-// a full tile of HBM reads in flight while it computes.
+// "tiles" of 4096 contiguous complex values (4096/N whole transforms), 16
+// values per lane.  Every transform is owned by TPF = N/16 lanes.  Each wave
+// reads its quarter of the tile with 16-byte non-temporal loads and
+// redistributes it through LDS into the first pass's layout; the output
+// leaves the same way, so all global traffic is fully coalesced dwordx4.
 //
 //   N <= 1024: each wave owns 1024/N whole transforms and a private LDS
-//              region, synchronised at wave scope.  For N < 1024 the wave's
-//              1024 contiguous input values are read with 16-byte loads and
-//              redistributed through LDS (and the same on the way out), so
-//              global traffic is fully coalesced.
+//              region, synchronised at wave scope (no workgroup barriers).
 //   N >= 2048: a transform spans 2 or 4 waves and passes synchronise the
 //              workgroup.
+//
+// A workgroup walks `tiles_per_block` consecutive tiles; kPrefetch keeps the
+// next tile's loads in flight while the current one is transformed.
 //
 // Twiddles W_{LR}^{j*k} of every Stockham pass depend only on the lane, so
 // each lane computes its (at most 30) factors once from the device table
@@ -48,7 +48,6 @@ struct C2CPlan {
     static constexpr int kR2 = N / (kR0 * kR1);   // 1 when two passes suffice
     static constexpr int kRLast = kR2 > 1 ? kR2 : kR1;
     static constexpr bool kWaveLocal = kTPF <= 64;
-    static constexpr bool kStaged = kTPF < 64;
     static constexpr int kSlot = N + N / 16;      // padded LDS slots per transform
     static constexpr int kLdsSlots = kFPB * kSlot;
     static constexpr int kTw1 = (16 / kR1) * (kR1 - 1);                  // pass-1 factors per lane
@@ -111,33 +110,38 @@ __device__ __forceinline__ void stockham_pass(cpx (&v)[16], cpx* slot, int t, co
     }
 }
 
-// Raw per-lane input of one tile, as loaded from global memory.
-//   staged:     16/kVec 16-byte vectors of kVec consecutive values each;
-//   not staged: 16 single values (8 or 4 bytes).
-template <class IO, int N>
+// Raw per-lane input of one tile as loaded from global memory: 16/kVec
+// 16-byte vectors of kVec consecutive complex values.  Lane l of wave w
+// holds tile elements 1024*w + kVec*l + 64*kVec*i, i < 16/kVec.
+template <class IO>
 struct TileRaw {
-    using P = C2CPlan<N>;
-    using W = std::conditional_t<P::kStaged, typename Io<IO>::W4, typename Io<IO>::W1>;
-    static constexpr int kCount = P::kStaged ? 16 / Io<IO>::kVec : 16;
+    using W = typename Io<IO>::W4;
+    static constexpr int kCount = 16 / Io<IO>::kVec;
     W w[kCount];
 };
 
-template <class IO, int N, bool FWD>
+// Every tile is 4096 contiguous complex values (kFPB whole transforms).
+// Tile element e lives in LDS at lds_pad(e) while it is staged, which is
+// also where transform f's element i sits in its slot (f*kSlot + lds_pad(i)).
+//
+// kPrefetch: keep the next tile's loads in flight while transforming the
+// current one (costs 2*16/kVec*4 VGPRs; pays off when occupancy is low).
+template <class IO, int N, bool FWD, bool kPrefetch>
 __global__ __launch_bounds__(256) void c2c_kernel(const IO* __restrict__ in, IO* __restrict__ out,
                                                   int batch, const float2* __restrict__ tw,
                                                   int tiles_per_block) {
     using P = C2CPlan<N>;
     using I = Io<IO>;
-    using Raw = TileRaw<IO, N>;
+    using Raw = TileRaw<IO>;
+    using W = typename Raw::W;
     __shared__ cpx lds[P::kLdsSlots];
     const int tid = threadIdx.x;
     const int f = tid / P::kTPF;  // transform slot within the tile
     const int t = tid % P::kTPF;  // lane within the transform
     const int wave = tid >> 6, lane = tid & 63;
-    constexpr int kFPW = P::kStaged ? 64 / P::kTPF : 1;  // transforms per wave (staged)
     constexpr int kVec = I::kVec;
     cpx* slot = lds + f * P::kSlot;
-    cpx* chunk = lds + wave * kFPW * P::kSlot;  // staged: the wave's 1024 values
+    cpx* chunk = lds + wave * (1024 + 64);  // the wave's quarter of the tile
 
     cpx w1[P::kTw1];
     cpx w2[P::kTw2 > 0 ? P::kTw2 : 1];
@@ -149,57 +153,49 @@ __global__ __launch_bounds__(256) void c2c_kernel(const IO* __restrict__ in, IO*
     const long long tile_end = tile + tiles_per_block < ntiles ? tile + tiles_per_block : ntiles;
     if (tile >= tile_end) return;  // uniform over the workgroup
 
-    // Number of valid values in this wave's staged chunk (0..1024), and
-    // whether this lane's transform exists (not staged).
-    auto staged_valid = [&](long long tl) {
-        const long long left = static_cast<long long>(batch) - (tl * P::kFPB + wave * kFPW);
-        return left <= 0 ? 0 : (left >= kFPW ? 1024 : static_cast<int>(left) * N);
+    // Valid values (0..1024) in this wave's quarter of tile tl: the tile's
+    // last transforms may lie past the batch.
+    auto chunk_valid = [&](long long tl) {
+        long long left = static_cast<long long>(batch) - tl * P::kFPB;
+        left = left < P::kFPB ? left : P::kFPB;
+        const long long v = left * N - 1024LL * wave;
+        return v <= 0 ? 0 : (v >= 1024 ? 1024 : static_cast<int>(v));
     };
     auto load_tile = [&](Raw& r, long long tl) {
-        if constexpr (P::kStaged) {
-            const int valid = staged_valid(tl);
-            const IO* src = in + (tl * P::kFPB + wave * kFPW) * N;
+        const int valid = chunk_valid(tl);
+        const IO* src = in + tl * P::kTile + 1024 * wave;
 #pragma unroll
-            for (int i = 0; i < Raw::kCount; ++i) {
-                const int e = kVec * lane + 64 * kVec * i;
-                r.w[i] = e < valid ? ld_nt(reinterpret_cast<const typename Raw::W*>(src + e))
-                                   : typename Raw::W{};
-            }
-        } else {
-            const bool active = tl * P::kFPB + f < batch;
-            const IO* src = in + (tl * P::kFPB + f) * N + t;
-#pragma unroll
-            for (int j = 0; j < 16; ++j)
-                r.w[j] = active ? ld_nt(reinterpret_cast<const typename Raw::W*>(src + j * P::kTPF))
-                                : typename Raw::W{};
+        for (int i = 0; i < Raw::kCount; ++i) {
+            const int e = kVec * lane + 64 * kVec * i;
+            r.w[i] = e < valid ? ld_nt(reinterpret_cast<const W*>(src + e)) : W{};
         }
     };
 
     Raw next;
-    load_tile(next, tile);
+    if constexpr (kPrefetch) load_tile(next, tile);
     for (; tile < tile_end; ++tile) {
-        const Raw cur = next;
-        if (tile + 1 < tile_end) load_tile(next, tile + 1);
-
-        // ---- pass-0 inputs x[t + j*TPF], j < 16 ----
-        cpx v[16];
-        if constexpr (P::kStaged) {
-            wave_lds_sync();  // the previous tile's reads of this region are done
-#pragma unroll
-            for (int i = 0; i < Raw::kCount; ++i) {
-                const int e = kVec * lane + 64 * kVec * i;
-                cpx q[kVec];
-                I::decode4(cur.w[i], q);
-#pragma unroll
-                for (int c = 0; c < kVec; ++c) chunk[lds_pad(e + c)] = q[c];
-            }
-            wave_lds_sync();
-#pragma unroll
-            for (int j = 0; j < 16; ++j) v[j] = slot[lds_pad(t + j * P::kTPF)];
+        Raw cur;
+        if constexpr (kPrefetch) {
+            cur = next;
+            if (tile + 1 < tile_end) load_tile(next, tile + 1);
         } else {
-#pragma unroll
-            for (int j = 0; j < 16; ++j) v[j] = I::decode1(cur.w[j]);
+            load_tile(cur, tile);
         }
+
+        // ---- stage: tile -> LDS, then pass-0 inputs x[t + j*TPF], j < 16 ----
+        region_sync<P::kWaveLocal>();  // the previous tile's reads of the region are done
+#pragma unroll
+        for (int i = 0; i < Raw::kCount; ++i) {
+            const int e = kVec * lane + 64 * kVec * i;
+            cpx q[kVec];
+            I::decode4(cur.w[i], q);
+#pragma unroll
+            for (int c = 0; c < kVec; ++c) chunk[lds_pad(e + c)] = q[c];
+        }
+        region_sync<P::kWaveLocal>();
+        cpx v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = slot[lds_pad(t + j * P::kTPF)];
 
         // ---- pass 0: radix 16 over stride-TPF inputs (L = 1, no twiddle) ----
         Dft<16, FWD>::run(v);
@@ -210,38 +206,24 @@ __global__ __launch_bounds__(256) void c2c_kernel(const IO* __restrict__ in, IO*
 
         // ---- store: last pass output m of butterfly b = t + TPF*q is y[b + m*N/RLast] ----
         constexpr int kRL = P::kRLast;
-        if constexpr (P::kStaged) {
-            wave_lds_sync();
+        region_sync<P::kWaveLocal>();
 #pragma unroll
-            for (int q = 0; q < 16 / kRL; ++q) {
-                const int b = t + P::kTPF * q;
+        for (int q = 0; q < 16 / kRL; ++q) {
+            const int b = t + P::kTPF * q;
 #pragma unroll
-                for (int m = 0; m < kRL; ++m) slot[lds_pad(b + m * (N / kRL))] = v[q * kRL + m];
-            }
-            wave_lds_sync();
-            const int valid = staged_valid(tile);
-            IO* dst = out + (tile * P::kFPB + wave * kFPW) * N;
+            for (int m = 0; m < kRL; ++m) slot[lds_pad(b + m * (N / kRL))] = v[q * kRL + m];
+        }
+        region_sync<P::kWaveLocal>();
+        const int valid = chunk_valid(tile);
+        IO* dst = out + tile * P::kTile + 1024 * wave;
 #pragma unroll
-            for (int i = 0; i < Raw::kCount; ++i) {
-                const int e = kVec * lane + 64 * kVec * i;
-                if (e < valid) {
-                    cpx q[kVec];
+        for (int i = 0; i < Raw::kCount; ++i) {
+            const int e = kVec * lane + 64 * kVec * i;
+            if (e < valid) {
+                cpx q[kVec];
 #pragma unroll
-                    for (int c = 0; c < kVec; ++c) q[c] = chunk[lds_pad(e + c)];
-                    st_nt(reinterpret_cast<typename Raw::W*>(dst + e), I::encode4(q));
-                }
-            }
-        } else {
-            if (tile * P::kFPB + f < batch) {
-                IO* dst = out + (tile * P::kFPB + f) * N;
-#pragma unroll
-                for (int q = 0; q < 16 / kRL; ++q) {
-                    const int b = t + P::kTPF * q;
-#pragma unroll
-                    for (int m = 0; m < kRL; ++m)
-                        st_nt(reinterpret_cast<typename Raw::W*>(dst + b + m * (N / kRL)),
-                              I::encode1(v[q * kRL + m]));
-                }
+                for (int c = 0; c < kVec; ++c) q[c] = chunk[lds_pad(e + c)];
+                st_nt(reinterpret_cast<W*>(dst + e), I::encode4(q));
             }
         }
     }

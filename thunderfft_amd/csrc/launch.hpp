@@ -16,15 +16,6 @@ hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, in
 // Transforms per tile (4096 complex values, one workgroup pass) for length N.
 int c2c_transforms_per_block(int n);
 
-// Tiles each workgroup walks: enough workgroups for about eight per compute
-// unit, at most 16 tiles each, so the hardware dispatcher balances the tail.
-inline int c2c_tiles_per_block(long long ntiles, int num_cus) {
-    const long long target = static_cast<long long>(num_cus > 0 ? num_cus : 256) * 8;
-    long long tpb = ntiles / target;
-    if (tpb < 1) tpb = 1;
-    if (tpb > 16) tpb = 16;
-    return static_cast<int>(tpb);
-}
 
 hipError_t launch_fill_uniform(int precision, void* out, long long count, unsigned long long seed,
                                long long first_element, hipStream_t stream);
