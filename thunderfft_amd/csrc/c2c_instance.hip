@@ -2,6 +2,7 @@
 // (compiled once per length, -DTHFF_N=64 ... 4096, so the lengths build in
 // parallel).
 #include "fft_c2c.hpp"
+#include "fft_mfma.hpp"
 #include "launch.hpp"
 
 #ifndef THFF_N
@@ -10,37 +11,66 @@
 
 namespace thff {
 
-// Tiles per workgroup, measured on MI355X at batch = 2^26/N (one tile per
-// workgroup leaves the most waves resident; two amortise the per-lane
-// twiddle setup where a tile holds few transforms).
+// Launch shape per (N, precision), from sweeps on MI355X at batch = 2^26/N
+// with random inputs: tiles each workgroup walks, and whether the next
+// tile's loads are issued before the current tile is transformed.
+struct LaunchShape {
+    int tiles;
+    bool prefetch;
+};
+
 template <int N>
-constexpr int preferred_tiles(int precision) {
-    return precision == 0 && N <= 1024 ? 1 : 2;
+constexpr LaunchShape launch_shape(int precision) {
+    if (precision == 0) {
+        if (N <= 256) return {1, false};
+        if (N <= 1024) return {2, true};
+        return {2, false};
+    }
+    if (N <= 256 || N == 2048) return {2, false};
+    if (N == 1024) return {2, false};  // the MFMA kernel
+    if (N <= 1024) return {2, true};
+    return {8, true};
+}
+
+template <class IO, int N, bool FWD>
+void enqueue(const LaunchShape& shape, unsigned grid, const IO* x, IO* y, int batch,
+             const float2* tw, int tpb, hipStream_t stream) {
+    if (shape.prefetch)
+        c2c_kernel<IO, N, FWD, true><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
+    else
+        c2c_kernel<IO, N, FWD, false><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
 }
 
 template <int N>
 hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, int batch,
                       const float2* tw, int num_cus, hipStream_t stream) {
     using P = C2CPlan<N>;
+    const LaunchShape shape = launch_shape<N>(precision);
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
     // Small batches spread one tile per workgroup over the whole device.
-    const int tpb = ntiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? preferred_tiles<N>(precision) : 1;
+    const int tpb = ntiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? shape.tiles : 1;
     const unsigned grid = static_cast<unsigned>((ntiles + tpb - 1) / tpb);
-    const dim3 block(P::kWG);
     if (precision == 0) {
         const auto* x = static_cast<const float2*>(in);
         auto* y = static_cast<float2*>(out);
         if (forward)
-            c2c_kernel<float2, N, true, false><<<grid, block, 0, stream>>>(x, y, batch, tw, tpb);
+            enqueue<float2, N, true>(shape, grid, x, y, batch, tw, tpb, stream);
         else
-            c2c_kernel<float2, N, false, false><<<grid, block, 0, stream>>>(x, y, batch, tw, tpb);
+            enqueue<float2, N, false>(shape, grid, x, y, batch, tw, tpb, stream);
     } else {
         const auto* x = static_cast<const __half2*>(in);
         auto* y = static_cast<__half2*>(out);
-        if (forward)
-            c2c_kernel<__half2, N, true, false><<<grid, block, 0, stream>>>(x, y, batch, tw, tpb);
-        else
-            c2c_kernel<__half2, N, false, false><<<grid, block, 0, stream>>>(x, y, batch, tw, tpb);
+        if constexpr (N == 1024) {
+            // radix-16 stages on MFMA (fft_mfma.hpp); same tile size as c2c_kernel
+            if (forward)
+                c2c_mfma1024_kernel<true, false><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
+            else
+                c2c_mfma1024_kernel<false, false><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
+        } else if (forward) {
+            enqueue<__half2, N, true>(shape, grid, x, y, batch, tw, tpb, stream);
+        } else {
+            enqueue<__half2, N, false>(shape, grid, x, y, batch, tw, tpb, stream);
+        }
     }
     return hipGetLastError();
 }
