@@ -1,17 +1,24 @@
 #!/usr/bin/env python3
-"""Benchmark of the hot path: batched C2C FFT, N=1024, batch 65536 (config 2).
+"""Benchmark of the hot path: batched C2C FFT, N=1024, batch 65536.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--cpu-seconds S]
 
 One step = one ThunderFFT_global launch (the C ABI's asynchronous entry,
-thff_global_async) over the whole batch, inputs resident in HBM.  Prints one
-JSON line: value = GFLOP/s (5 N log2 N per transform) of the float forward
-transform; the half and inverse transforms are reported under "also".
+thff_global_async) over the whole batch of 65536 signals of N=1024, inputs
+resident in HBM (generated on the device by thff_fill_uniform).  After W
+untimed steps, K steps run back to back between two HIP events recorded on
+the launch stream, bracketed by device synchronisation; ms_per_step is the
+event time / K.  value = GFLOP/s (5 N log2 N per transform) of the float
+forward transform; the inverse and the half transforms are measured the same
+way and reported under "also".
+
 roofline.achieved = algorithmic bytes per launch (read + write of every
-complex value once: 2 * batch * N * sizeof(T)) / mean kernel duration, the
-duration measured with HIP events recorded around each launch on the launch
-stream.  cpu_baseline = the oracle's fp32 four-step port (the reference has no
-CPU path) timed on this host's cores on a bounded sample of the same workload.
+complex value once: 2 * batch * N * sizeof(T)) / the mean launch duration
+above; roofline.traffic = HBM bytes per launch from the rocprofv3 FETCH_SIZE /
+WRITE_SIZE runs summarised in profiles/ (each scaled by what the counter reads
+for a plain copy of known size).  cpu_baseline = the oracle's threaded fp32
+four-step (the reference has no CPU FFT) timed on this host's cores on a
+bounded sample of the same workload.
 """
 from __future__ import annotations
 
@@ -19,21 +26,22 @@ import argparse
 import json
 import math
 import os
+import re
 import sys
 import time
 
 HBM_PEAK_GBPS = 8000.0
 N_FFT = 1024
 BATCH = 65536
-PROFILE_TRAFFIC = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "traffic_c2c_n1024.json")
+ROOT = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "pmc_c2c_n1024_b65536.md")
 
 
 def parse():
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target wall time of the CPU baseline sample")
@@ -55,29 +63,26 @@ def time_gpu(T: str, forward: bool, steps: int, warmup: int) -> dict:
     thff.ThunderFFTInitialize(T, n)
     for _ in range(warmup):
         thff.ThunderFFT_global_async(T, n, forward, x, y, batch, stream)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     t0 = time.perf_counter()
-    for i in range(steps):
-        starts[i].record(stream)
+    start.record(stream)
+    for _ in range(steps):
         thff.ThunderFFT_global_async(T, n, forward, x, y, batch, stream)
-        ends[i].record(stream)
+    end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))  # ms
-    mean_ms = sum(per) / len(per)
-    median_ms = per[len(per) // 2]
+    ms = start.elapsed_time(end) / steps
     nbytes = 2 * n * batch * elem
     flops = 5.0 * n * math.log2(n) * batch
     del x, y
     return {
         "precision": T, "direction": "forward" if forward else "inverse",
-        "us_per_call": mean_ms * 1e3, "us_per_call_median": median_ms * 1e3,
-        "us_per_transform": mean_ms * 1e3 / batch,
-        "gflops": flops / (mean_ms * 1e-3) / 1e9,
-        "gbps": nbytes / (mean_ms * 1e-3) / 1e9,
-        "pct_hbm_peak": 100.0 * nbytes / (mean_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+        "us_per_call": ms * 1e3, "us_per_transform": ms * 1e3 / batch,
+        "gflops": flops / (ms * 1e-3) / 1e9,
+        "gbps": nbytes / (ms * 1e-3) / 1e9,
+        "pct_hbm_peak": 100.0 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
         "bytes_per_call": nbytes, "wall_s": wall,
     }
 
@@ -89,7 +94,7 @@ def copy_bandwidth() -> float:
     a = torch.empty(64 << 20, dtype=torch.float64, device="cuda")
     b = torch.empty_like(a)
     a.fill_(1.0)
-    for _ in range(3):
+    for _ in range(10):
         b.copy_(a)
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -107,8 +112,6 @@ def copy_bandwidth() -> float:
 def cpu_baseline(target_s: float) -> dict:
     """The oracle's fp32 four-step (restating the reference's radix-4 64x16
     split) on this host's cores, on a bounded sample of the N=1024 workload."""
-    import numpy as np
-
     import oracle
 
     cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
@@ -126,8 +129,7 @@ def cpu_baseline(target_s: float) -> dict:
         if dt >= target_s / 4 or sample >= BATCH:
             break
         sample = min(BATCH, sample * max(2, int(target_s / 4 / max(dt, 1e-3))))
-    reps = max(1, int(target_s / max(dt, 1e-3)))
-    reps = min(reps, 8)
+    reps = max(1, min(8, int(target_s / max(dt, 1e-3))))
     t0 = time.perf_counter()
     for _ in range(reps):
         oracle.fft_f32_fourstep(x, True, cores)
@@ -137,17 +139,19 @@ def cpu_baseline(target_s: float) -> dict:
     return {"value": flops / dt / 1e9, "unit": "GFLOP/s", "cores": cores, "kind": "port",
             "sample": f"{sample} float forward transforms of N={n} (of the {BATCH}-signal "
                       f"workload), {reps} timed passes, {dt * 1e3:.1f} ms per pass, "
-                      f"oracle fft_f32_fourstep",
+                      f"oracle fft_f32_fourstep on {cores} threads",
             "us_per_transform": dt * 1e6 / sample}
 
 
-def load_traffic():
+def load_traffic(key: str):
+    """HBM bytes per launch for `key` (e.g. float_fwd) from the PMC summary."""
     try:
-        with open(PROFILE_TRAFFIC) as f:
-            d = json.load(f)
-        return d.get("hbm_bytes_per_launch")
-    except (OSError, ValueError):
+        with open(TRAFFIC_PROFILE) as f:
+            text = f.read()
+    except OSError:
         return None
+    m = re.search(rf"^hbm_bytes_per_launch {re.escape(key)}: (\d+)\s*$", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 def main():
@@ -202,13 +206,15 @@ def main():
         "copy_gbps": round(copy_gbps, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": load_traffic(),
-                     "kernel": "thff::c2c_kernel<float2,1024,true>",
+                     "traffic": load_traffic("float_fwd"),
+                     "kernel": "thff::c2c_kernel<float2,1024,true,true>",
                      "algorithmic_bytes": main_run["bytes_per_call"]},
         "cpu_baseline": cpu,
         "also": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
                      for kk, vv in v.items()} for k, v in runs.items()},
     }
+    for k in out["also"]:
+        out["also"][k]["hbm_traffic_bytes"] = load_traffic(k)
     print(json.dumps(out), flush=True)
 
 
