@@ -77,6 +77,25 @@ int thff_global(int precision, int n, int forward, const void* d_input, void* d_
 int thff_global_async(int precision, int n, int forward, const void* d_input, void* d_output,
                       int batch, void* stream);
 
+/* Fused circular convolution (no function counterpart in the reference
+ * library; the reference ships it as the sample kernel
+ * thunder_convN_block_kernel_realin_realout,
+ * sample/conv1d/conv1d_fullfft_l4096_thunder.cu:280-331, which this
+ * generalises to complex signals, all seven lengths and per-signal filters):
+ *   y[b][k] = sum_m x[b][m] * h[f][(k - m) mod n],  f = per_signal_filter ? b : 0,
+ * computed as IFFT(FFT(x[b]) * FFT(h[f])) / n in one kernel (forward FFT,
+ * pointwise product, inverse FFT and the 1/n scale; the spectra stay on chip).
+ * x and y hold batch*n complex values, h holds batch*n (per-signal) or n
+ * (shared) values, all in `precision` storage, natural order.  Same checks and
+ * return codes as thff_global (y may alias neither x nor h), requires
+ * thff_initialize(precision, n), synchronises `stream` before returning. */
+int thff_conv1d(int precision, int n, const void* d_x, const void* d_h, void* d_y, int batch,
+                int per_signal_filter, void* stream);
+
+/* thff_conv1d without the final stream synchronisation. */
+int thff_conv1d_async(int precision, int n, const void* d_x, const void* d_h, void* d_y,
+                      int batch, int per_signal_filter, void* stream);
+
 /* Snapshot of the current device's twiddle cache for `precision`: the device
  * pointer (NULL when released) and its length (0 when released).  The
  * reference exposes the same state through its device symbols

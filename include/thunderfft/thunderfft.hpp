@@ -85,4 +85,18 @@ inline void ThunderFFT_global(vec2_t<T>* d_input, vec2_t<T>* d_output, int batch
                               batch, static_cast<void*>(stream)));
 }
 
+// Fused circular convolution y[b] = IFFT(FFT(x[b]) * FFT(h[b or 0])) / N of
+// `batch` signals of N values (per-signal filters, or one shared filter).
+// No counterpart in the reference's library API; the reference ships the
+// fused convolution as a sample kernel
+// (sample/conv1d/conv1d_fullfft_l4096_thunder.cu:280-331).  Same argument
+// checks and synchronous semantics as ThunderFFT_global; Initialize<T>(N) first.
+template <typename T, int N>
+inline void ThunderFFT_conv1d(const vec2_t<T>* d_x, const vec2_t<T>* d_h, vec2_t<T>* d_y,
+                              int batch, bool per_signal_filter = true, hipStream_t stream = 0) {
+    static_assert(is_supported_length<N>, "Unsupported ThunderFFT length");
+    detail::check(thff_conv1d(detail::precision_code<T>(), N, d_x, d_h, d_y, batch,
+                              per_signal_filter ? 1 : 0, static_cast<void*>(stream)));
+}
+
 }  // namespace thunderfft

@@ -72,3 +72,18 @@ def test_cpp_template_api_host_only():
     assert "18 checks passed before any HIP calls" in res.stderr
     bad = subprocess.run([exe, "--bogus"], capture_output=True, text=True, env=env, timeout=60)
     assert bad.returncode == 2
+
+
+def test_conv1d_argument_checks():
+    """thff_conv1d rejects bad arguments before any HIP call (same rules as
+    ThunderFFT_global, plus: the output may alias neither input)."""
+    with pytest.raises(ValueError, match="nonnegative"):
+        thff.ThunderFFT_conv1d("float", 64, 8, 16, 24, -1)
+    thff.ThunderFFT_conv1d("float", 64, 0, 0, 0, 0)  # zero batch: no-op
+    for args in ((0, 16, 24), (8, 0, 24), (8, 16, 0), (8, 16, 8), (8, 16, 16)):
+        with pytest.raises(ValueError):
+            thff.ThunderFFT_conv1d("float", 64, *args, 1)
+    with pytest.raises(ValueError, match="Unsupported"):
+        thff.ThunderFFT_conv1d("float", 96, 8, 16, 24, 1)
+    with pytest.raises(ValueError):
+        thff.ThunderFFT_conv1d("double", 64, 8, 16, 24, 1)

@@ -24,7 +24,7 @@ import os
 __all__ = [
     "SUPPORTED_N", "PRECISIONS", "lib", "ThunderFFTInitialize", "ThunderFFTFinalize",
     "ThunderFFT_global", "ThunderFFT_global_async", "twiddle_info", "fill_uniform",
-    "fft", "transforms_per_block", "LIB_PATH",
+    "fft", "transforms_per_block", "LIB_PATH", "ThunderFFT_conv1d", "ThunderFFT_conv1d_async",
 ]
 
 SUPPORTED_N = (64, 128, 256, 512, 1024, 2048, 4096)
@@ -53,6 +53,9 @@ def lib() -> ctypes.CDLL:
         sig = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, ctypes.c_int, vp]
         L.thff_global.argtypes = sig
         L.thff_global_async.argtypes = sig
+        csig = [ctypes.c_int, ctypes.c_int, vp, vp, vp, ctypes.c_int, ctypes.c_int, vp]
+        L.thff_conv1d.argtypes = csig
+        L.thff_conv1d_async.argtypes = csig
         L.thff_twiddle_info.argtypes = [ctypes.c_int, ctypes.POINTER(vp),
                                         ctypes.POINTER(ctypes.c_int)]
         L.thff_fill_uniform.argtypes = [ctypes.c_int, vp, ctypes.c_longlong, ctypes.c_ulonglong,
@@ -123,6 +126,20 @@ def ThunderFFT_global_async(T, N: int, forward: bool, d_input, d_output, batch: 
     """As ThunderFFT_global, but returns once the launch is enqueued on ``stream``."""
     _raise(lib().thff_global_async(_precision(T), int(N), int(bool(forward)), _ptr(d_input),
                                    _ptr(d_output), int(batch), _stream(stream)))
+
+
+def ThunderFFT_conv1d(T, N: int, d_x, d_h, d_y, batch: int, per_signal_filter: bool = True,
+                      stream=0) -> None:
+    """Fused circular convolution y[b] = IFFT(FFT(x[b]) * FFT(h[b or 0])) / N; synchronous."""
+    _raise(lib().thff_conv1d(_precision(T), int(N), _ptr(d_x), _ptr(d_h), _ptr(d_y), int(batch),
+                             int(bool(per_signal_filter)), _stream(stream)))
+
+
+def ThunderFFT_conv1d_async(T, N: int, d_x, d_h, d_y, batch: int, per_signal_filter: bool = True,
+                            stream=0) -> None:
+    """As ThunderFFT_conv1d, but returns once the launch is enqueued on ``stream``."""
+    _raise(lib().thff_conv1d_async(_precision(T), int(N), _ptr(d_x), _ptr(d_h), _ptr(d_y),
+                                   int(batch), int(bool(per_signal_filter)), _stream(stream)))
 
 
 def twiddle_info(T) -> tuple[int, int]:

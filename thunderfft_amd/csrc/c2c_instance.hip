@@ -2,6 +2,7 @@
 // (compiled once per length, -DTHFF_N=64 ... 4096, so the lengths build in
 // parallel).
 #include "fft_c2c.hpp"
+#include "fft_conv.hpp"
 #include "fft_mfma.hpp"
 #include "launch.hpp"
 
@@ -75,7 +76,36 @@ hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, in
     return hipGetLastError();
 }
 
+template <class IO, int N>
+void enqueue_conv1d(bool per_signal, unsigned grid, const IO* x, const IO* h, IO* y, int batch,
+                    const float2* tw, int tpb, hipStream_t stream) {
+    if (per_signal)
+        conv1d_kernel<IO, N, true><<<grid, 256, 0, stream>>>(x, h, y, batch, tw, tpb);
+    else
+        conv1d_kernel<IO, N, false><<<grid, 256, 0, stream>>>(x, h, y, batch, tw, tpb);
+}
+
+template <int N>
+hipError_t launch_conv1d(int precision, bool per_signal_filter, const void* x, const void* h,
+                         void* y, int batch, const float2* tw, int num_cus, hipStream_t stream) {
+    using P = C2CPlan<N>;
+    const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
+    const int tpb = ntiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? 2 : 1;
+    const unsigned grid = static_cast<unsigned>((ntiles + tpb - 1) / tpb);
+    if (precision == 0)
+        enqueue_conv1d<float2, N>(per_signal_filter, grid, static_cast<const float2*>(x),
+                                  static_cast<const float2*>(h), static_cast<float2*>(y), batch, tw,
+                                  tpb, stream);
+    else
+        enqueue_conv1d<__half2, N>(per_signal_filter, grid, static_cast<const __half2*>(x),
+                                   static_cast<const __half2*>(h), static_cast<__half2*>(y), batch,
+                                   tw, tpb, stream);
+    return hipGetLastError();
+}
+
 template hipError_t launch_c2c<THFF_N>(int, bool, const void*, void*, int, const float2*, int,
                                        hipStream_t);
+template hipError_t launch_conv1d<THFF_N>(int, bool, const void*, const void*, void*, int,
+                                          const float2*, int, hipStream_t);
 
 }  // namespace thff

@@ -80,6 +80,70 @@ hipError_t dispatch(int n, int precision, bool forward, const void* in, void* ou
     }
 }
 
+hipError_t dispatch_conv1d(int n, int precision, bool per_signal, const void* x, const void* h,
+                           void* y, int batch, const float2* tw, int cus, hipStream_t s) {
+    switch (n) {
+    case 64: return thff::launch_conv1d<64>(precision, per_signal, x, h, y, batch, tw, cus, s);
+    case 128: return thff::launch_conv1d<128>(precision, per_signal, x, h, y, batch, tw, cus, s);
+    case 256: return thff::launch_conv1d<256>(precision, per_signal, x, h, y, batch, tw, cus, s);
+    case 512: return thff::launch_conv1d<512>(precision, per_signal, x, h, y, batch, tw, cus, s);
+    case 1024: return thff::launch_conv1d<1024>(precision, per_signal, x, h, y, batch, tw, cus, s);
+    case 2048: return thff::launch_conv1d<2048>(precision, per_signal, x, h, y, batch, tw, cus, s);
+    case 4096: return thff::launch_conv1d<4096>(precision, per_signal, x, h, y, batch, tw, cus, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// The current device's cached table for (precision, n) and its CU count, or
+// an error message naming the missing ThunderFFTInitialize call.
+int cached_table(int precision, int n, const char* who, const float2** table, int* cus) {
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return fail_hip(err, "hipGetDevice");
+    {
+        std::lock_guard<std::mutex> lock(g_mutex[precision]);
+        const auto found = g_cache[precision].find(device);
+        if (found != g_cache[precision].end() && found->second.n == n) {
+            *table = found->second.table;
+            *cus = found->second.num_cus;
+            return THFF_OK;
+        }
+    }
+    return fail(THFF_EIO, std::string("[ThunderFFT] ") + who + ": no twiddle table for N=" +
+                              std::to_string(n) + " on device " + std::to_string(device) +
+                              "; call ThunderFFTInitialize<" + precision_name(precision) + ">(" +
+                              std::to_string(n) + ") first");
+}
+
+int conv1d_impl(int precision, int n, const void* x, const void* h, void* y, int batch,
+                int per_signal_filter, void* stream, bool synchronize) {
+    if (!supported_precision(precision))
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d supports float and half only");
+    if (!supported_length(n)) return fail(THFF_EINVAL, "Unsupported ThunderFFT length");
+    if (batch < 0) return fail(THFF_EINVAL, "ThunderFFT batch must be nonnegative");
+    if (batch == 0) return THFF_OK;
+    if (!x || !h || !y)
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d requires non-null signal, filter and output");
+    if (y == x || y == h)
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d output must not alias its inputs");
+    const long long fpb = thff::c2c_transforms_per_block(n);
+    if ((static_cast<long long>(batch) + fpb - 1) / fpb * 256 > static_cast<long long>(UINT32_MAX))
+        return fail(THFF_EINVAL, "ThunderFFT batch exceeds one launch for this length");
+    const float2* table = nullptr;
+    int cus = 0;
+    const int rc = cached_table(precision, n, "ThunderFFT_conv1d", &table, &cus);
+    if (rc != THFF_OK) return rc;
+    auto s = static_cast<hipStream_t>(stream);
+    hipError_t err = dispatch_conv1d(n, precision, per_signal_filter != 0, x, h, y, batch, table,
+                                     cus, s);
+    if (err != hipSuccess) return fail_hip(err, "ThunderFFT_conv1d launch");
+    if (synchronize) {
+        err = hipStreamSynchronize(s);
+        if (err != hipSuccess) return fail_hip(err, "ThunderFFT_conv1d synchronize");
+    }
+    return THFF_OK;
+}
+
 int global_impl(int precision, int n, int forward, const void* d_input, void* d_output, int batch,
                 void* stream, bool synchronize) {
     if (!supported_precision(precision))
@@ -196,6 +260,16 @@ int thff_global(int precision, int n, int forward, const void* d_input, void* d_
 int thff_global_async(int precision, int n, int forward, const void* d_input, void* d_output,
                       int batch, void* stream) {
     return global_impl(precision, n, forward, d_input, d_output, batch, stream, false);
+}
+
+int thff_conv1d(int precision, int n, const void* d_x, const void* d_h, void* d_y, int batch,
+                int per_signal_filter, void* stream) {
+    return conv1d_impl(precision, n, d_x, d_h, d_y, batch, per_signal_filter, stream, true);
+}
+
+int thff_conv1d_async(int precision, int n, const void* d_x, const void* d_h, void* d_y,
+                      int batch, int per_signal_filter, void* stream) {
+    return conv1d_impl(precision, n, d_x, d_h, d_y, batch, per_signal_filter, stream, false);
 }
 
 int thff_twiddle_info(int precision, const void** d_table, int* n) {

@@ -13,6 +13,12 @@ template <int N>
 hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, int batch,
                       const float2* tw, int num_cus, hipStream_t stream);
 
+// Enqueue the fused circular convolution of `batch` signals of length N:
+// y[b] = IFFT(FFT(x[b]) * FFT(h[per_signal_filter ? b : 0])) / N.
+template <int N>
+hipError_t launch_conv1d(int precision, bool per_signal_filter, const void* x, const void* h,
+                         void* y, int batch, const float2* tw, int num_cus, hipStream_t stream);
+
 // Transforms per tile (4096 complex values, one workgroup pass) for length N.
 int c2c_transforms_per_block(int n);
 
