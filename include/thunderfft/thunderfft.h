@@ -96,6 +96,25 @@ int thff_conv1d(int precision, int n, const void* d_x, const void* d_h, void* d_
 int thff_conv1d_async(int precision, int n, const void* d_x, const void* d_h, void* d_y,
                       int batch, int per_signal_filter, void* stream);
 
+/* Fused 2-D circular convolution of `batch` rows x cols row-major images with
+ * one shared rows x cols filter (no function counterpart in the reference
+ * library; the reference's 2-D convolution is the sample
+ * sample/conv2d/thunder.cu:70-207,556-565, row FFT -> column FFT x H ->
+ * column IFFT -> row IFFT over one 1024 x 1024 image, and the unbuilt 64 x 64
+ * tile sketch sample/conv2d/thunder_tile64.cu:33-208):
+ *   y[b][r][c] = sum_{r',c'} x[b][r'][c'] * h[(r - r') mod rows][(c - c') mod cols],
+ * computed as IFFT2(FFT2(x[b]) * FFT2(h)) / (rows*cols) in one kernel per
+ * image.  rows = cols = 64 (THFF_EINVAL otherwise); requires
+ * thff_initialize(precision, 64).  x and y hold batch*rows*cols complex
+ * values, h rows*cols.  Same checks, return codes and synchronisation as
+ * thff_conv1d. */
+int thff_conv2d(int precision, int rows, int cols, const void* d_x, const void* d_h, void* d_y,
+                int batch, void* stream);
+
+/* thff_conv2d without the final stream synchronisation. */
+int thff_conv2d_async(int precision, int rows, int cols, const void* d_x, const void* d_h,
+                      void* d_y, int batch, void* stream);
+
 /* Snapshot of the current device's twiddle cache for `precision`: the device
  * pointer (NULL when released) and its length (0 when released).  The
  * reference exposes the same state through its device symbols

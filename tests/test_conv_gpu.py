@@ -122,3 +122,73 @@ def test_config4_conv1d_2048(T):
     assert np.isfinite(err) and err <= TIGHT[T]
     del x, y, h, imp
     torch.cuda.empty_cache()
+
+
+def _filter2d(seed, full=False):
+    """BASELINE config 5 filter: real 64 x 64, nonzero 7 x 7 corner block with
+    i.i.d. N(0, 1/7) taps (full=True: every tap nonzero, complex)."""
+    rng = np.random.default_rng(seed)
+    h = np.zeros((64, 64), dtype=np.complex64)
+    if full:
+        h[:] = (rng.normal(0, 1 / 64, (64, 64)) + 1j * rng.normal(0, 1 / 64, (64, 64)))
+    else:
+        h[:7, :7] = rng.normal(0.0, 1.0 / 7.0, (7, 7))
+    return h
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+def test_conv2d_matches_direct_convolution(T):
+    import thunderfft_amd as thff
+
+    thff.ThunderFFTInitialize(T, 64)
+    for batch, full in ((1, False), (3, True), (2, False)):
+        x = oracle.uniform(4096, batch, seed=77 + batch).reshape(batch, 64, 64)
+        h = _filter2d(batch, full)
+        xr, hr = oracle.represent(x, T), oracle.represent(h, T)
+        d_x, d_h = to_device(xr, T), to_device(hr, T)
+        d_y = to_device(np.full((batch, 64, 64), np.nan, dtype=np.complex64), T)
+        thff.ThunderFFT_conv2d(T, 64, 64, d_x, d_h, d_y, batch)
+        y = from_device(d_y, T).reshape(batch, 64, 64)
+        m = oracle.metrics(y, oracle.circconv2d(xr, hr))
+        label = f"{T} conv2d 64x64 batch={batch} full_filter={full}: rel_l2={m['rel_l2']:.3e}"
+        print(label, flush=True)
+        assert m["nonfinite"] == 0, label
+        assert m["rel_l2"] <= GATE and m["rel_l2"] <= TIGHT[T], label
+
+
+def test_config5_conv2d_64x64():
+    """8192 float2 images of 64 x 64, shared 7 x 7-corner filter."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    T, batch = "float", 8192
+    seed = oracle.BENCH_SEED_BASE + 4096
+    x = torch.empty(2 * 4096 * batch, dtype=torch.float32, device="cuda")
+    thff.fill_uniform(T, x, 4096 * batch, seed)
+    y = torch.empty_like(x)
+    thff.ThunderFFTInitialize(T, 64)
+
+    # (1) the config-5 filter on a subset of images against the direct convolution
+    h = _filter2d(5)
+    thff.ThunderFFT_conv2d(T, 64, 64, x, to_device(h, T), y, batch)
+    rows = np.array([0, 1, 2047, 4096, 6000, batch - 2, batch - 1])
+    sub = from_device(y.view(batch, 2 * 4096)[torch.from_numpy(rows).cuda()].contiguous(), T)
+    xin = np.concatenate([oracle.uniform(4096, 1, seed, first_element=int(r) * 4096)
+                          for r in rows]).reshape(len(rows), 64, 64)
+    m = oracle.metrics(sub.reshape(len(rows), 64, 64), oracle.circconv2d(xin, h))
+    print(f"conv2d 64x64 batch={batch} subset rel_l2={m['rel_l2']:.3e}", flush=True)
+    assert m["nonfinite"] == 0 and m["rel_l2"] <= GATE and m["rel_l2"] <= TIGHT[T]
+
+    # (2) every image: a unit impulse at (dr, dc) rolls every image by (dr, dc)
+    dr, dc = 5, 61
+    imp = np.zeros((64, 64), dtype=np.complex64)
+    imp[dr, dc] = 1
+    thff.ThunderFFT_conv2d(T, 64, 64, x, to_device(imp, T), y, batch)
+    want = torch.roll(x.view(batch, 64, 64, 2), shifts=(dr, dc), dims=(1, 2))
+    err = float(torch.linalg.vector_norm(y.view(batch, 64, 64, 2) - want) /
+                torch.linalg.vector_norm(want))
+    print(f"  impulse roll over all images rel_l2={err:.3e}", flush=True)
+    assert np.isfinite(err) and err <= TIGHT[T]
+    del x, y
+    torch.cuda.empty_cache()

@@ -87,3 +87,15 @@ def test_conv1d_argument_checks():
         thff.ThunderFFT_conv1d("float", 96, 8, 16, 24, 1)
     with pytest.raises(ValueError):
         thff.ThunderFFT_conv1d("double", 64, 8, 16, 24, 1)
+
+
+def test_conv2d_argument_checks():
+    """thff_conv2d: 64 x 64 only; the rest as thff_conv1d, before any HIP call."""
+    with pytest.raises(ValueError, match="64 x 64"):
+        thff.ThunderFFT_conv2d("float", 32, 64, 8, 16, 24, 1)
+    with pytest.raises(ValueError, match="nonnegative"):
+        thff.ThunderFFT_conv2d("float", 64, 64, 8, 16, 24, -1)
+    thff.ThunderFFT_conv2d("float", 64, 64, 0, 0, 0, 0)  # zero batch: no-op
+    for args in ((0, 16, 24), (8, 0, 24), (8, 16, 0), (8, 16, 8), (8, 16, 16)):
+        with pytest.raises(ValueError):
+            thff.ThunderFFT_conv2d("float", 64, 64, *args, 1)

@@ -25,6 +25,7 @@ __all__ = [
     "SUPPORTED_N", "PRECISIONS", "lib", "ThunderFFTInitialize", "ThunderFFTFinalize",
     "ThunderFFT_global", "ThunderFFT_global_async", "twiddle_info", "fill_uniform",
     "fft", "transforms_per_block", "LIB_PATH", "ThunderFFT_conv1d", "ThunderFFT_conv1d_async",
+    "ThunderFFT_conv2d", "ThunderFFT_conv2d_async",
 ]
 
 SUPPORTED_N = (64, 128, 256, 512, 1024, 2048, 4096)
@@ -56,6 +57,9 @@ def lib() -> ctypes.CDLL:
         csig = [ctypes.c_int, ctypes.c_int, vp, vp, vp, ctypes.c_int, ctypes.c_int, vp]
         L.thff_conv1d.argtypes = csig
         L.thff_conv1d_async.argtypes = csig
+        c2sig = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, vp, ctypes.c_int, vp]
+        L.thff_conv2d.argtypes = c2sig
+        L.thff_conv2d_async.argtypes = c2sig
         L.thff_twiddle_info.argtypes = [ctypes.c_int, ctypes.POINTER(vp),
                                         ctypes.POINTER(ctypes.c_int)]
         L.thff_fill_uniform.argtypes = [ctypes.c_int, vp, ctypes.c_longlong, ctypes.c_ulonglong,
@@ -140,6 +144,19 @@ def ThunderFFT_conv1d_async(T, N: int, d_x, d_h, d_y, batch: int, per_signal_fil
     """As ThunderFFT_conv1d, but returns once the launch is enqueued on ``stream``."""
     _raise(lib().thff_conv1d_async(_precision(T), int(N), _ptr(d_x), _ptr(d_h), _ptr(d_y),
                                    int(batch), int(bool(per_signal_filter)), _stream(stream)))
+
+
+def ThunderFFT_conv2d(T, rows: int, cols: int, d_x, d_h, d_y, batch: int, stream=0) -> None:
+    """Fused 2-D circular convolution y[b] = IFFT2(FFT2(x[b]) * FFT2(h)) / (rows*cols);
+    64 x 64 images, one shared filter; synchronous."""
+    _raise(lib().thff_conv2d(_precision(T), int(rows), int(cols), _ptr(d_x), _ptr(d_h), _ptr(d_y),
+                             int(batch), _stream(stream)))
+
+
+def ThunderFFT_conv2d_async(T, rows: int, cols: int, d_x, d_h, d_y, batch: int, stream=0) -> None:
+    """As ThunderFFT_conv2d, but returns once the launch is enqueued on ``stream``."""
+    _raise(lib().thff_conv2d_async(_precision(T), int(rows), int(cols), _ptr(d_x), _ptr(d_h),
+                                   _ptr(d_y), int(batch), _stream(stream)))
 
 
 def twiddle_info(T) -> tuple[int, int]:

@@ -103,6 +103,26 @@ hipError_t launch_conv1d(int precision, bool per_signal_filter, const void* x, c
     return hipGetLastError();
 }
 
+#if THFF_N == 64
+hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y, int batch,
+                           const float2* tw, int num_cus, hipStream_t stream) {
+    // One image per tile; a workgroup transforms the filter once, so it
+    // walks several images when the batch is large.
+    const long long tiles = batch;
+    const int tpb = tiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? 8 : 1;
+    const unsigned grid = static_cast<unsigned>((tiles + tpb - 1) / tpb);
+    if (precision == 0)
+        conv2d64_kernel<float2><<<grid, 256, 0, stream>>>(static_cast<const float2*>(x),
+                                                          static_cast<const float2*>(h),
+                                                          static_cast<float2*>(y), batch, tw, tpb);
+    else
+        conv2d64_kernel<__half2><<<grid, 256, 0, stream>>>(static_cast<const __half2*>(x),
+                                                           static_cast<const __half2*>(h),
+                                                           static_cast<__half2*>(y), batch, tw, tpb);
+    return hipGetLastError();
+}
+#endif
+
 template hipError_t launch_c2c<THFF_N>(int, bool, const void*, void*, int, const float2*, int,
                                        hipStream_t);
 template hipError_t launch_conv1d<THFF_N>(int, bool, const void*, const void*, void*, int,

@@ -144,6 +144,33 @@ int conv1d_impl(int precision, int n, const void* x, const void* h, void* y, int
     return THFF_OK;
 }
 
+int conv2d_impl(int precision, int rows, int cols, const void* x, const void* h, void* y,
+                int batch, void* stream, bool synchronize) {
+    if (!supported_precision(precision))
+        return fail(THFF_EINVAL, "ThunderFFT_conv2d supports float and half only");
+    if (rows != 64 || cols != 64)
+        return fail(THFF_EINVAL, "ThunderFFT_conv2d supports 64 x 64 images only");
+    if (batch < 0) return fail(THFF_EINVAL, "ThunderFFT batch must be nonnegative");
+    if (batch == 0) return THFF_OK;
+    if (!x || !h || !y)
+        return fail(THFF_EINVAL, "ThunderFFT_conv2d requires non-null images, filter and output");
+    if (y == x || y == h)
+        return fail(THFF_EINVAL, "ThunderFFT_conv2d output must not alias its inputs");
+    if (batch > (1 << 24)) return fail(THFF_EINVAL, "ThunderFFT batch exceeds one launch");
+    const float2* table = nullptr;
+    int cus = 0;
+    const int rc = cached_table(precision, 64, "ThunderFFT_conv2d", &table, &cus);
+    if (rc != THFF_OK) return rc;
+    auto s = static_cast<hipStream_t>(stream);
+    hipError_t err = thff::launch_conv2d64(precision, x, h, y, batch, table, cus, s);
+    if (err != hipSuccess) return fail_hip(err, "ThunderFFT_conv2d launch");
+    if (synchronize) {
+        err = hipStreamSynchronize(s);
+        if (err != hipSuccess) return fail_hip(err, "ThunderFFT_conv2d synchronize");
+    }
+    return THFF_OK;
+}
+
 int global_impl(int precision, int n, int forward, const void* d_input, void* d_output, int batch,
                 void* stream, bool synchronize) {
     if (!supported_precision(precision))
@@ -270,6 +297,16 @@ int thff_conv1d(int precision, int n, const void* d_x, const void* d_h, void* d_
 int thff_conv1d_async(int precision, int n, const void* d_x, const void* d_h, void* d_y,
                       int batch, int per_signal_filter, void* stream) {
     return conv1d_impl(precision, n, d_x, d_h, d_y, batch, per_signal_filter, stream, false);
+}
+
+int thff_conv2d(int precision, int rows, int cols, const void* d_x, const void* d_h, void* d_y,
+                int batch, void* stream) {
+    return conv2d_impl(precision, rows, cols, d_x, d_h, d_y, batch, stream, true);
+}
+
+int thff_conv2d_async(int precision, int rows, int cols, const void* d_x, const void* d_h,
+                      void* d_y, int batch, void* stream) {
+    return conv2d_impl(precision, rows, cols, d_x, d_h, d_y, batch, stream, false);
 }
 
 int thff_twiddle_info(int precision, const void** d_table, int* n) {

@@ -158,7 +158,8 @@ struct TileRaw {
     W w[kCount];
 };
 
-// Moves 4096-value tiles between HBM and the pass layout.  Tile element e
+// Moves 4096-value tiles between HBM and the pass layout (`batch` counts
+// transforms of length N).  Tile element e
 // sits at LDS position lds_pad(e) while staged, which is also where transform
 // f's element i sits in its slot (f*kSlot + lds_pad(i)).  The last tile of a
 // batch may hold fewer than kFPB transforms: missing inputs read as zero and
@@ -180,15 +181,15 @@ struct TileIO {
           slot(lds + (tid / P::kTPF) * P::kSlot), chunk(lds + (tid >> 6) * (1024 + 64)) {}
 
     // Valid values (0..1024) in this wave's quarter of tile tl.
-    __device__ __forceinline__ int valid(long long tl, int batch) const {
-        long long left = static_cast<long long>(batch) - tl * P::kFPB;
+    __device__ __forceinline__ int valid(long long tl, long long batch) const {
+        long long left = batch - tl * P::kFPB;
         left = left < P::kFPB ? left : P::kFPB;
         const long long v = left * N - 1024LL * wave;
         return v <= 0 ? 0 : (v >= 1024 ? 1024 : static_cast<int>(v));
     }
 
     __device__ __forceinline__ void load(Raw& r, const IO* __restrict__ base, long long tl,
-                                         int batch) const {
+                                         long long batch) const {
         const int nv = valid(tl, batch);
         const IO* src = base + tl * P::kTile + 1024 * wave;
 #pragma unroll
@@ -216,7 +217,7 @@ struct TileIO {
 
     // v[j] = y[t + TPF*j] -> LDS -> 16-byte non-temporal stores of tile tl.
     __device__ __forceinline__ void store(const cpx (&v)[16], IO* __restrict__ base, long long tl,
-                                          int batch) const {
+                                          long long batch) const {
         region_sync<P::kWaveLocal>();
 #pragma unroll
         for (int j = 0; j < 16; ++j) slot[lds_pad(t + j * P::kTPF)] = v[j];

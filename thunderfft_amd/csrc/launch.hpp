@@ -19,6 +19,11 @@ template <int N>
 hipError_t launch_conv1d(int precision, bool per_signal_filter, const void* x, const void* h,
                          void* y, int batch, const float2* tw, int num_cus, hipStream_t stream);
 
+// Enqueue the fused 2-D circular convolution of `batch` 64 x 64 images with
+// one shared 64 x 64 filter h (tw: the N = 64 table).
+hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y, int batch,
+                           const float2* tw, int num_cus, hipStream_t stream);
+
 // Transforms per tile (4096 complex values, one workgroup pass) for length N.
 int c2c_transforms_per_block(int n);
 
