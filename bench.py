@@ -87,6 +87,67 @@ def time_gpu(T: str, forward: bool, steps: int, warmup: int) -> dict:
     }
 
 
+def time_conv(kind: str, T: str, steps: int, warmup: int) -> dict:
+    """BASELINE config 4 (conv1d: 16384 signals of 2048, per-signal complex
+    filters with N(0, 1/sqrt(2048)) taps) or config 5 (conv2d: 8192 64 x 64
+    images, one shared real filter with a N(0, 1/7) 7 x 7 corner block)."""
+    import numpy as np
+    import torch
+
+    import thunderfft_amd as thff
+
+    dt = torch.float32 if T == "float" else torch.float16
+    elem = 8 if T == "float" else 4
+    gen = torch.Generator(device="cuda").manual_seed(2048)
+    if kind == "conv1d":
+        n, batch = 2048, 16384
+        count = n * batch
+        h = (torch.randn(2 * count, device="cuda", generator=gen) / math.sqrt(n)).to(dt)
+        nbytes = 3 * count * elem
+        flops = 3 * 5.0 * n * math.log2(n) * batch + 6.0 * count
+        init_n = n
+    else:
+        n, batch = 4096, 8192
+        count = n * batch
+        hh = np.zeros((64, 64, 2), dtype=np.float32)
+        hh[:7, :7, 0] = np.random.default_rng(7).normal(0.0, 1.0 / 7.0, (7, 7))
+        h = torch.from_numpy(hh.reshape(-1)).to(device="cuda", dtype=dt)
+        nbytes = 2 * count * elem
+        flops = 2 * 2 * 64 * 5.0 * 64 * math.log2(64) * batch + 6.0 * count
+        init_n = 64
+    x = torch.empty(2 * count, dtype=dt, device="cuda")
+    y = torch.empty_like(x)
+    stream = torch.cuda.current_stream()
+    thff.fill_uniform(T, x, count, 0x7F4A7C15 + n, 0, stream)
+    thff.ThunderFFTInitialize(T, init_n)
+
+    def launch():
+        if kind == "conv1d":
+            thff.ThunderFFT_conv1d_async(T, n, x, h, y, batch, True, stream)
+        else:
+            thff.ThunderFFT_conv2d_async(T, 64, 64, x, h, y, batch, stream)
+
+    for _ in range(warmup):
+        launch()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        launch()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    thff.ThunderFFTFinalize(T)
+    del x, y, h
+    return {"workload": (f"{kind} {batch} x {'2048' if kind == 'conv1d' else '64x64'} "
+                         f"{T}2, fused FFT * H * IFFT"),
+            "precision": T, "us_per_call": ms * 1e3, "gflops": flops / (ms * 1e-3) / 1e9,
+            "gbps": nbytes / (ms * 1e-3) / 1e9,
+            "pct_hbm_peak": 100.0 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+            "bytes_per_call": nbytes}
+
+
 def copy_bandwidth() -> float:
     """Device-to-device copy of a 512 MiB buffer (read + write), GB/s."""
     import torch
@@ -180,6 +241,12 @@ def main():
                   f"{r['gflops']:.0f} GFLOP/s", file=sys.stderr, flush=True)
     thff.ThunderFFTFinalize("float")
     thff.ThunderFFTFinalize("half")
+    for kind, T in (("conv1d", "float"), ("conv1d", "half"), ("conv2d", "float")):
+        r = time_conv(kind, T, max(1, a.steps // 2), max(1, a.warmup // 2))
+        runs[f"{kind}_{T}"] = r
+        print(f"[bench] {r['workload']}: {r['us_per_call']:.1f} us, {r['gbps']:.0f} GB/s "
+              f"({r['pct_hbm_peak']:.1f}% of HBM peak), {r['gflops']:.0f} GFLOP/s",
+              file=sys.stderr, flush=True)
     copy_gbps = copy_bandwidth()
     main_run = runs["float_fwd"]
     cpu = None if a.no_cpu else cpu_baseline(a.cpu_seconds)
@@ -215,6 +282,9 @@ def main():
     }
     for k in out["also"]:
         out["also"][k]["hbm_traffic_bytes"] = load_traffic(k)
+    out["also"]["conv_note"] = ("conv1d bytes = x, h and y (3 * 2^25 complex); conv2d bytes = x "
+                                "and y (2 * 2^25 complex; the 32 KiB filter is read per "
+                                "workgroup from L2); GFLOP/s counts 5 N log2 N per transform")
     print(json.dumps(out), flush=True)
 
 
