@@ -3,7 +3,8 @@
     python -m thunderfft_amd.build [--jobs J] [--verbose]
 
 Every kernel translation unit is compiled for gfx950 only, with packed FP32
-instructions disabled (-Xclang -target-feature -Xclang -packed-fp32-ops).  The
+instructions disabled (-Xclang -target-feature -Xclang -packed-fp32-ops) and
+MFMA results kept in VGPRs (-mllvm -amdgpu-mfma-vgpr-form).  The
 per-length kernel file is compiled once per transform length so the lengths
 build in parallel.  Objects go to thunderfft_amd/_build/, the shared library
 to thunderfft_amd/libthunderfft_amd.so (loaded by thunderfft_amd/__init__.py).
@@ -37,6 +38,8 @@ def common_flags() -> list[str]:
     return [
         f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA results in ordinary VGPRs (no AGPR round trip through v_accvgpr_read)
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         "-I", os.path.join(ROOT, "include"), "-I", CSRC,
     ]
 

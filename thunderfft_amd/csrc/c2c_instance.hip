@@ -22,15 +22,10 @@ struct LaunchShape {
 
 template <int N>
 constexpr LaunchShape launch_shape(int precision) {
-    if (precision == 0) {
-        if (N <= 256) return {1, false};
-        if (N <= 1024) return {2, true};
-        return {2, false};
-    }
-    if (N <= 256 || N == 2048) return {2, false};
-    if (N == 1024) return {2, false};  // the MFMA kernel
-    if (N <= 1024) return {2, true};
-    return {8, true};
+    if (precision == 0) return N == 2048 ? LaunchShape{2, true} : LaunchShape{1, false};
+    if (N <= 128) return {1, false};
+    if (N <= 512) return {2, false};
+    return {2, true};  // N = 1024 runs the MFMA kernel
 }
 
 template <class IO, int N, bool FWD>
@@ -64,9 +59,9 @@ hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, in
         if constexpr (N == 1024) {
             // radix-16 stages on MFMA (fft_mfma.hpp); same tile size as c2c_kernel
             if (forward)
-                c2c_mfma1024_kernel<true, false><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
+                c2c_mfma1024_kernel<true, true><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
             else
-                c2c_mfma1024_kernel<false, false><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
+                c2c_mfma1024_kernel<false, true><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
         } else if (forward) {
             enqueue<__half2, N, true>(shape, grid, x, y, batch, tw, tpb, stream);
         } else {

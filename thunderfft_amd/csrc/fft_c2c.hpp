@@ -20,10 +20,15 @@
 
 namespace thff {
 
+// Lengths up to 1024 are held to <= 168 VGPRs (3 waves per SIMD) without
+// spilling; the longer ones keep the compiler's choice.
+template <int N>
+inline constexpr int kMinWavesPerEU = N <= 1024 ? 3 : 1;
+
 template <class IO, int N, bool FWD, bool kPrefetch>
-__global__ __launch_bounds__(256) void c2c_kernel(const IO* __restrict__ in, IO* __restrict__ out,
-                                                  int batch, const float2* __restrict__ tw,
-                                                  int tiles_per_block) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kMinWavesPerEU<N>))) void
+c2c_kernel(const IO* __restrict__ in, IO* __restrict__ out, int batch, const float2* __restrict__ tw,
+           int tiles_per_block) {
     using P = C2CPlan<N>;
     using T = TileIO<IO, N>;
     __shared__ cpx lds[P::kLdsSlots];

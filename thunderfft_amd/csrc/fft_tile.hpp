@@ -24,10 +24,8 @@
 // are multiplied by W_{L*R}^{j*k}, an R-point DFT gives outputs y_m written to
 // (b - k)*R + k + m*L.
 //
-// Twiddles W_{LR}^{j*k} depend only on the lane, so each lane loads its (at
-// most 30) factors once and keeps them in registers; they are stored with the
-// positive angle and conjugated at use for the forward direction, so one set
-// serves both directions.
+// Twiddles W_{LR}^{j*k} depend only on the lane: each lane loads a few base
+// factors once (PassTwiddles) and keeps them in registers.
 #pragma once
 
 #include "fft_core.hpp"
@@ -51,8 +49,6 @@ struct C2CPlan {
     static constexpr bool kWaveLocal = kTPF <= 64;
     static constexpr int kSlot = N + N / 16;      // padded LDS slots per transform
     static constexpr int kLdsSlots = kFPB * kSlot;
-    static constexpr int kTw1 = (16 / kR1) * (kR1 - 1);                  // pass-1 factors per lane
-    static constexpr int kTw2 = kR2 > 1 ? (16 / kR2) * (kR2 - 1) : 0;   // pass-2 factors per lane
 };
 
 __device__ __forceinline__ int lds_pad(int i) { return i + (i >> 4); }
@@ -65,40 +61,71 @@ __device__ __forceinline__ void region_sync() {
         __syncthreads();
 }
 
-// Per-lane twiddles of the pass of radix R that follows sub-transforms of
-// length L: for butterfly b = t + TPF*q (q < 16/R) and input j (1 <= j < R),
-// (cos, sin)(2*pi*j*(b mod L)/(L*R)), read from the fp32 table
-// tw[m] = (cos, sin)(2*pi*m/N) (positive angle, as the reference's table,
-// thunderfft_impl_twiddle.cuh:76-91).
+// Twiddles of the pass of radix R that follows sub-transforms of length L.
+// Butterfly b = t + TPF*q (q < 16/R) multiplies input j by W_{LR}^{j*k},
+// k = b mod L.  Whenever q > 0 occurs, t + TPF*q < L and L*R = 16*TPF, so
+// W_{LR}^{j*k} = W_{LR}^{j*(t mod L)} * W_16^{j*q}: only the lane's base
+// factors W_{LR}^{j*(t mod L)} are kept in registers and W_16^{j*q} is a
+// compile-time rotation.  For R = 16 the 15 bases are rebuilt per use from
+// 6 stored ones, W^{(4a+c)k} = W^{4ak} * W^{ck}.  Values carry the positive
+// angle (cos, sin)(2*pi*m/N) of the fp32 table (as the reference's table,
+// thunderfft_impl_twiddle.cuh:76-91) and are conjugated at use for the
+// forward direction, so one set serves both directions.
 template <int N, int R, int L>
-__device__ __forceinline__ void pass_twiddles(cpx* w, int t, const float2* __restrict__ tw) {
-    using P = C2CPlan<N>;
-#pragma unroll
-    for (int q = 0; q < 16 / R; ++q) {
-        const int k = (t + P::kTPF * q) % L;
-#pragma unroll
-        for (int j = 1; j < R; ++j) {
+struct PassTwiddles {
+    static constexpr bool kCompact = R == 16;
+    static constexpr int kStored = kCompact ? 6 : R - 1;
+    cpx b[kStored];
+
+    __device__ __forceinline__ void load(int t, const float2* __restrict__ tw) {
+        const int k = t % L;
+        auto w = [&](int j) {
             const float2 x = tw[(j * k * (N / (L * R))) & (N - 1)];
-            w[q * (R - 1) + j - 1] = cpx{x.x, x.y};
+            return cpx{x.x, x.y};
+        };
+        if constexpr (kCompact) {
+            b[0] = w(1), b[1] = w(2), b[2] = w(3);
+            b[3] = w(4), b[4] = w(8), b[5] = w(12);
+        } else {
+#pragma unroll
+            for (int j = 1; j < R; ++j) b[j - 1] = w(j);
         }
     }
-}
+
+    // All R-1 bases W_{LR}^{j*(t mod L)}, j = 1..R-1.
+    __device__ __forceinline__ void expand(cpx* w) const {
+        if constexpr (kCompact) {
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int j = 4 * a + c;
+                    if (j == 0) continue;
+                    w[j - 1] = a == 0 ? b[c - 1] : (c == 0 ? b[2 + a] : cmul(b[2 + a], b[c - 1]));
+                }
+        } else {
+#pragma unroll
+            for (int j = 0; j < R - 1; ++j) w[j] = b[j];
+        }
+    }
+};
 
 template <int N>
 struct LaneTwiddles {
     using P = C2CPlan<N>;
-    cpx w1[P::kTw1];
-    cpx w2[P::kTw2 > 0 ? P::kTw2 : 1];
+    PassTwiddles<N, P::kR1, 16> p1;
+    PassTwiddles<N, (P::kR2 > 1 ? P::kR2 : 2), 16 * P::kR1> p2;  // unused when kR2 == 1
     __device__ __forceinline__ void load(int t, const float2* __restrict__ tw) {
-        pass_twiddles<N, P::kR1, 16>(w1, t, tw);
-        if constexpr (P::kR2 > 1) pass_twiddles<N, P::kR2, 16 * P::kR1>(w2, t, tw);
+        p1.load(t, tw);
+        if constexpr (P::kR2 > 1) p2.load(t, tw);
     }
 };
 
 // One Stockham pass p >= 1: write the previous pass's outputs to LDS, read
 // this pass's inputs, twiddle, DFT.
 template <int N, bool FWD, int R, int L, int RPrev, int LPrev>
-__device__ __forceinline__ void stockham_pass(cpx (&v)[16], cpx* slot, int t, const cpx* w) {
+__device__ __forceinline__ void stockham_pass(cpx (&v)[16], cpx* slot, int t,
+                                              const PassTwiddles<N, R, L>& tw) {
     using P = C2CPlan<N>;
     // previous outputs: butterfly b = t + TPF*q, output m -> (b/LPrev)*LPrev*RPrev + b%LPrev + m*LPrev
     region_sync<P::kWaveLocal>();
@@ -110,21 +137,19 @@ __device__ __forceinline__ void stockham_pass(cpx (&v)[16], cpx* slot, int t, co
         for (int m = 0; m < RPrev; ++m) slot[lds_pad(base + m * LPrev)] = v[q * RPrev + m];
     }
     region_sync<P::kWaveLocal>();
-#pragma unroll
-    for (int q = 0; q < 16 / R; ++q) {
+    cpx w[R - 1];
+    tw.expand(w);
+    static_for<0, 16 / R>([&](auto qc) {
+        constexpr int q = decltype(qc)::value;
         const int b = t + P::kTPF * q;
-#pragma unroll
-        for (int j = 0; j < R; ++j) {
+        v[q * R] = slot[lds_pad(b)];
+        static_for<1, R>([&](auto jc) {
+            constexpr int j = decltype(jc)::value;
             const cpx x = slot[lds_pad(b + j * (N / R))];
-            if (j == 0) {
-                v[q * R] = x;
-            } else {
-                const cpx ww = w[q * (R - 1) + j - 1];
-                v[q * R + j] = FWD ? cmulc(x, ww) : cmul(x, ww);
-            }
-        }
+            v[q * R + j] = rot<16, j * q, FWD>(FWD ? cmulc(x, w[j - 1]) : cmul(x, w[j - 1]));
+        });
         Dft<R, FWD>::run(v + q * R);
-    }
+    });
 }
 
 // The whole transform of the lane's transform slot: v[j] = x[t + TPF*j] in,
@@ -134,8 +159,8 @@ __device__ __forceinline__ void fft_registers(cpx (&v)[16], cpx* slot, int t,
                                               const LaneTwiddles<N>& w) {
     using P = C2CPlan<N>;
     Dft<16, FWD>::run(v);
-    stockham_pass<N, FWD, P::kR1, 16, 16, 1>(v, slot, t, w.w1);
-    if constexpr (P::kR2 > 1) stockham_pass<N, FWD, P::kR2, 16 * P::kR1, P::kR1, 16>(v, slot, t, w.w2);
+    stockham_pass<N, FWD, P::kR1, 16, 16, 1>(v, slot, t, w.p1);
+    if constexpr (P::kR2 > 1) stockham_pass<N, FWD, P::kR2, 16 * P::kR1, P::kR1, 16>(v, slot, t, w.p2);
     // last pass: output m of butterfly b = t + TPF*q is X[b + m*N/RLast]
     //          = X[t + TPF*(q + m*16/RLast)]
     constexpr int kRL = P::kRLast;
