@@ -71,6 +71,18 @@ void ThunderFFTFinalize() {
     detail::check(thff_finalize(detail::precision_code<T>()));
 }
 
+// Device pointer of the current device's twiddle table for T (the table
+// ThunderFFT_kernel_reg / ThunderFFT_load_twiddles read), nullptr when
+// released.  The reference exposes the same state through its device symbols
+// d_twiddle_{f,h} (detail/thunderfft_impl_twiddle.cuh:44-68).
+template <typename T>
+inline const float2* ThunderFFT_twiddle_table() {
+    const void* table = nullptr;
+    int n = 0;
+    detail::check(thff_twiddle_info(detail::precision_code<T>(), &table, &n));
+    return static_cast<const float2*>(table);
+}
+
 // Batched unnormalized out-of-place C2C FFT of `batch` natural-order signals
 // of N values (signal j at offset j*N).  forward = exp(-2*pi*i*k/N).
 // batch < 0, null or identical pointers throw std::invalid_argument; batch 0

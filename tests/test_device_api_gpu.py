@@ -1,0 +1,114 @@
+"""GPU tests of the device-side fusion API (<thunderfft/thunderfft_device.hpp>).
+
+Kernels written against the public API the way a caller would
+(thunderfft_amd/apps/device_example.hip, built into
+thunderfft_amd/_build/libthff_device_example.so) are run through ctypes:
+
+* the reference's validate_core pattern (sample/validation/
+  fft_validation.cu:84-123): gmem -> smem (layout_t) -> fragment ->
+  ThunderFFT_kernel_reg -> smem -> gmem, with 64 workspace sentinels that must
+  survive;
+* the same through ThunderFFT_gmem2reg / reg2gmem only;
+* a fused forward FFT x per-bin filter x inverse FFT / N.
+
+Every length x {float, half} x {forward, inverse} against the fp64 oracle;
+the float results must also equal ThunderFFT_global's bit for bit (both run
+the same transform code).
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from thff_testlib import GATE, SIZES, TIGHT, from_device, to_device
+
+pytestmark = pytest.mark.gpu
+
+EXAMPLE = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                       "thunderfft_amd", "_build", "libthff_device_example.so")
+PREC = {"float": 0, "half": 1}
+
+
+@pytest.fixture(scope="module")
+def ex():
+    import torch
+
+    import thunderfft_amd as thff
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    thff.lib()
+    if not os.path.exists(EXAMPLE):
+        raise FileNotFoundError(f"{EXAMPLE} missing: run __graft_entry__.build()")
+    L = ctypes.CDLL(EXAMPLE)
+    vp, ci = ctypes.c_void_p, ctypes.c_int
+    L.thffx_device_fft.argtypes = [ci, ci, ci, vp, vp, ci, vp, vp]
+    L.thffx_device_fft_reg.argtypes = [ci, ci, ci, vp, vp, ci, vp]
+    L.thffx_fused_filter.argtypes = [ci, ci, vp, vp, vp, ci, vp]
+    yield L
+    thff.ThunderFFTFinalize("float")
+    thff.ThunderFFTFinalize("half")
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("n", SIZES)
+def test_device_api_fft(ex, T, n):
+    import torch
+
+    import thunderfft_amd as thff
+
+    bpb = thff.transforms_per_block(n)
+    batch = 2 * bpb
+    thff.ThunderFFTInitialize(T, n)
+    x = oracle.represent(oracle.uniform(n, batch, seed=31 + n), T)
+    d_x = to_device(x, T)
+    guard = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for forward in (True, False):
+        ref = oracle.fft(x, forward)
+        d_lib = torch.empty_like(d_x)
+        thff.ThunderFFT_global(T, n, forward, d_x, d_lib, batch)
+        for kind in ("smem", "reg"):
+            d_y = torch.full_like(d_x, float("nan"))
+            if kind == "smem":
+                rc = ex.thffx_device_fft(PREC[T], n, int(forward), d_x.data_ptr(), d_y.data_ptr(),
+                                         batch, guard.data_ptr(), None)
+            else:
+                rc = ex.thffx_device_fft_reg(PREC[T], n, int(forward), d_x.data_ptr(),
+                                             d_y.data_ptr(), batch, None)
+            assert rc == 0, (kind, rc)
+            y = from_device(d_y, T).reshape(batch, n)
+            m = oracle.metrics(y, ref)
+            label = f"device API ({kind}) {T} N={n} {'fwd' if forward else 'inv'}: rel_l2={m['rel_l2']:.3e}"
+            print(label, flush=True)
+            assert m["nonfinite"] == 0 and m["rel_l2"] <= GATE and m["rel_l2"] <= TIGHT[T], label
+            if T == "float":
+                assert torch.equal(d_y.view(torch.int32), d_lib.view(torch.int32)), label
+    assert int(guard.item()) == 0, "workspace sentinels changed"
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("n", [64, 1024, 4096])
+def test_device_api_fused_filter(ex, T, n):
+    import thunderfft_amd as thff
+
+    bpb = thff.transforms_per_block(n)
+    batch = 3 * bpb
+    thff.ThunderFFTInitialize(T, n)
+    x = oracle.represent(oracle.uniform(n, batch, seed=7 * n), T)
+    rng = np.random.default_rng(n)
+    H = (rng.normal(size=n) + 1j * rng.normal(size=n)).astype(np.complex64)
+    d_x = to_device(x, T)
+    d_h = to_device(H, "float")
+    d_y = to_device(np.full((batch, n), np.nan, dtype=np.complex64), T)
+    assert ex.thffx_fused_filter(PREC[T], n, d_x.data_ptr(), d_y.data_ptr(), d_h.data_ptr(),
+                                 batch, None) == 0
+    y = from_device(d_y, T).reshape(batch, n)
+    ref = oracle.fft(oracle.fft(x, True) * H.astype(np.complex128)[None, :], False) / n
+    m = oracle.metrics(y, ref)
+    label = f"device API fused filter {T} N={n}: rel_l2={m['rel_l2']:.3e}"
+    print(label, flush=True)
+    # half: the spectrum is also rounded to binary16 between the transforms
+    assert m["nonfinite"] == 0 and m["rel_l2"] <= GATE
+    assert m["rel_l2"] <= (5e-6 if T == "float" else 2e-3), label

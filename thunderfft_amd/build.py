@@ -90,6 +90,8 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
 
 
 APPS = ("thff_validate",)
+# Shared libraries of kernels written against the public device API (tests use them).
+DEVICE_EXAMPLES = ("device_example",)
 
 
 def build_apps(verbose: bool = False) -> list[str]:
@@ -107,6 +109,16 @@ def build_apps(verbose: bool = False) -> list[str]:
         if res.returncode != 0:
             raise RuntimeError(f"app build failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
         out.append(exe)
+    for ex in DEVICE_EXAMPLES:
+        so = os.path.join(BUILD, f"libthff_{ex}.so")
+        cmd = [cc, *common_flags(), "-shared", os.path.join(PKG, "apps", ex + ".hip"), "-o", so,
+               "-L", PKG, "-lthunderfft_amd", "-Wl,-rpath,$ORIGIN/.."]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"example build failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+        out.append(so)
     return out
 
 

@@ -1,9 +1,9 @@
 // c2c_instance.hip -- instantiates the C2C kernels of one length THFF_N
 // (compiled once per length, -DTHFF_N=64 ... 4096, so the lengths build in
 // parallel).
-#include "fft_c2c.hpp"
-#include "fft_conv.hpp"
-#include "fft_mfma.hpp"
+#include "thunderfft/detail/fft_c2c.hpp"
+#include "thunderfft/detail/fft_conv.hpp"
+#include "thunderfft/detail/fft_mfma.hpp"
 #include "launch.hpp"
 
 #ifndef THFF_N
