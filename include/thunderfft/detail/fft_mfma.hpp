@@ -22,7 +22,8 @@
 // and receives outputs 4q+i..; the rows of F are permuted so that lane group
 // q receives outputs k = q + 4r, r = 0..3 (r = 2*half + i/2, o = i%2).
 //
-// N = 1024 = 16 x 64, one wave per transform (x[t + 64 j], t < 64, j < 16):
+// The kernel below handles N = 256*C = 16 x (C x 16) for C in {1, 2, 4, 8};
+// for N = 1024 (C = 4) = 16 x 64, one wave per transform (x[t + 64 j], t < 64, j < 16):
 //   1. DFT16 over j for the 64 sequences t = 16c + n (c = column block 0..3)
 //      -> y[c][r] = Y_t[k1], k1 = q + 4r                      (16 MFMAs)
 //   2. y *= W_1024^(t*k1)                                     (per-lane constants)
@@ -92,24 +93,57 @@ __device__ __forceinline__ unsigned pack_half2(cpx v) {
 
 __device__ __forceinline__ f16x8 as_f16x8(u32x4 w) { return __builtin_bit_cast(f16x8, w); }
 
-struct MfmaPlan1024 {
-    static constexpr int N = 1024;
-    static constexpr int kFPB = 4;          // transforms per tile (one per wave)
-    static constexpr int kTile = 4096;      // complex values per tile
-    static constexpr int kRegion = 1280;    // LDS dwords per wave
-    static constexpr int kTw1 = 16 * 64;    // step-2 twiddles, [c][r][lane]
+// Plan of the MFMA kernel for N = 256*C = 16 x (C x 16), C in {1, 2, 4, 8}.
+template <int C>
+struct MfmaPlan {
+    static_assert(C == 1 || C == 2 || C == 4 || C == 8, "MFMA plan: C in {1, 2, 4, 8}");
+    static constexpr int N = 256 * C;              // transform length
+    static constexpr int kM = 16 * C;              // stride of the first DFT16's inputs (N/16)
+    static constexpr int kBlocks = C < 4 ? 4 : C;  // 16-sequence MFMA blocks per wave
+    static constexpr int kFPW = kBlocks / C;       // transforms per wave
+    static constexpr int kVals = 4 * kBlocks;      // complex values per lane
+    static constexpr int kWaveVals = 64 * kVals;   // values per wave (1024 or 2048)
+    static constexpr int kFPB = 4 * kFPW;          // transforms per tile (4 waves)
+    // LDS staging layouts (half2 units).  Input: pad kInPad after every
+    // kInPeriod values, so the stride-16C first-stage reads of the 64 lanes
+    // (n + 64C*q) hit 64 different banks.  Output: pad 16 after every C rows
+    // of 16 (C >= 2), so the final writes (n + 16C*q) do too.
+    static constexpr int kInPeriod = C <= 4 ? 64 : 128;
+    static constexpr int kInPad = C <= 4 ? 16 / C : 4;
+    static constexpr int kOutPeriod = 16 * C;
+    static constexpr int kOutPad = C == 1 ? 0 : 16;
+    static constexpr int kInSize = kWaveVals + kInPad * (kWaveVals / kInPeriod);
+    static constexpr int kOutSize = kWaveVals + kOutPad * (kWaveVals / kOutPeriod);
+    static constexpr int kRegion = kInSize > kOutSize ? kInSize : kOutSize;  // dwords per wave
+    static constexpr int kTw1 = C * 4 * 64;        // first twiddles, [c][r][lane]
+    __device__ static __forceinline__ int in_pad(int k) { return k + kInPad * (k / kInPeriod); }
+    __device__ static __forceinline__ int out_pad(int k) {
+        return k + kOutPad * (k / kOutPeriod);
+    }
 };
 
-// Padded LDS positions (in half2 units) of the staging layouts.
-__device__ __forceinline__ int in_pad(int k) { return k + 4 * (k >> 6); }
-__device__ __forceinline__ int out_pad(int k) { return k + 16 * (k >> 6); }
+// Batched C2C of half2 signals of N = 256*C on MFMA (C = 4 is N = 1024 as
+// described at the top of this file; in general N = 16 x (C x 16)):
+//   1. DFT16 over j of x[t + 16C j] for the 16C sequences t = 16c + n
+//   2. twiddle W_N^(t*k1), k1 = q + 4r   3. DFT_C over c (in-lane)
+//   4. twiddle W_16C^(n*m)               5. LDS transpose
+//   6. DFT16 over n -> X[k1 + 16 m + 16C (q' + 4 r')]
+// A wave owns 4/C transforms (C <= 4, 16 values per lane) or one (C = 8,
+// 32 values per lane); a workgroup of 4 waves walks tiles of 4 waves' worth.
+// C <= 4 is held to <= 128 VGPRs (4 waves per SIMD) without spilling.
+template <int C>
+inline constexpr int kMfmaMinWavesPerEU = C <= 4 ? 4 : 1;
 
-template <bool FWD, bool kPrefetch>
-__global__ __launch_bounds__(256) void c2c_mfma1024_kernel(const __half2* __restrict__ in,
-                                                           __half2* __restrict__ out, int batch,
-                                                           const float2* __restrict__ tw,
-                                                           int tiles_per_block) {
-    using P = MfmaPlan1024;
+template <int C, bool FWD, bool kPrefetch>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kMfmaMinWavesPerEU<C>))) void
+c2c_mfma_kernel(const __half2* __restrict__ in,
+                                                       __half2* __restrict__ out, int batch,
+                                                       const float2* __restrict__ tw,
+                                                       int tiles_per_block) {
+    using P = MfmaPlan<C>;
+    constexpr int N = P::N;
+    constexpr int kB = P::kBlocks;
+    constexpr int kRaw = P::kVals / 4;  // 16-byte loads per lane
     __shared__ unsigned lds[4 * P::kRegion];
     __shared__ cpx w1[P::kTw1];
     const int tid = threadIdx.x;
@@ -119,18 +153,18 @@ __global__ __launch_bounds__(256) void c2c_mfma1024_kernel(const __half2* __rest
 
     f16x8 a[2][2];
     dft16_operands<FWD>(a, lane);
-    // Step-2 twiddles W_1024^(t*k1), t = 16c + n, k1 = q + 4r, shared by the
-    // four waves through LDS (wave c fills column block c), and step-4
-    // twiddles W_64^(n*m) = W_1024^(16 n m); all from the positive-angle table.
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const float2 x = tw[((16 * wave + n) * (q + 4 * r)) & 1023];
-        w1[(wave * 4 + r) * 64 + lane] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+    // Step-2 twiddles W_N^(t*k1), t = 16c + n, k1 = q + 4r, shared through
+    // LDS; step-4 twiddles W_16C^(n*m) = W_N^(16 n m); both from the
+    // positive-angle table, conjugated here for the forward direction.
+    for (int e = tid; e < P::kTw1; e += 256) {
+        const int l = e & 63, r = (e >> 6) & 3, c = e >> 8;
+        const float2 x = tw[((16 * c + (l & 15)) * ((l >> 4) + 4 * r)) & (N - 1)];
+        w1[e] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
     }
-    cpx w2[3];
+    cpx w2[C > 1 ? C - 1 : 1];
 #pragma unroll
-    for (int m = 1; m < 4; ++m) {
-        const float2 x = tw[(16 * n * m) & 1023];
+    for (int m = 1; m < C; ++m) {
+        const float2 x = tw[(16 * n * m) & (N - 1)];
         w2[m - 1] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
     }
     __syncthreads();
@@ -140,89 +174,99 @@ __global__ __launch_bounds__(256) void c2c_mfma1024_kernel(const __half2* __rest
     const long long tile_end = tile + tiles_per_block < ntiles ? tile + tiles_per_block : ntiles;
     if (tile >= tile_end) return;  // uniform over the workgroup
 
-    // Each wave owns transform tile*4 + wave; it is valid or not as a whole.
-    auto load = [&](u32x4 (&r)[4], long long tl) {
-        const bool valid = tl * P::kFPB + wave < batch;
-        const __half2* src = in + (tl * P::kFPB + wave) * P::N;
+    // Valid values (0..kWaveVals) of this wave's kFPW transforms in tile tl.
+    auto valid = [&](long long tl) {
+        const long long v = (static_cast<long long>(batch) - tl * P::kFPB - wave * P::kFPW) * N;
+        return v <= 0 ? 0 : (v >= P::kWaveVals ? P::kWaveVals : static_cast<int>(v));
+    };
+    auto load = [&](u32x4 (&r)[kRaw], long long tl) {
+        const int nv = valid(tl);
+        const __half2* src = in + (tl * P::kFPB + wave * P::kFPW) * N;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            r[i] = valid ? ld_nt(reinterpret_cast<const u32x4*>(src + 4 * lane + 256 * i)) : u32x4{};
+        for (int i = 0; i < kRaw; ++i) {
+            const int e = 4 * lane + 256 * i;
+            r[i] = e < nv ? ld_nt(reinterpret_cast<const u32x4*>(src + e)) : u32x4{};
+        }
     };
 
-    u32x4 next[4];
+    u32x4 next[kRaw];
     if constexpr (kPrefetch) load(next, tile);
     for (; tile < tile_end; ++tile) {
-        u32x4 cur[4];
+        u32x4 cur[kRaw];
         if constexpr (kPrefetch) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) cur[i] = next[i];
+            for (int i = 0; i < kRaw; ++i) cur[i] = next[i];
             if (tile + 1 < tile_end) load(next, tile + 1);
         } else {
             load(cur, tile);
         }
 
-        // ---- stage the transform in LDS (natural order, 4 dwords pad per 64) ----
+        // ---- stage the wave's transforms in LDS (natural order, padded) ----
         wave_lds_sync();
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<u32x4*>(region + in_pad(4 * lane + 256 * i)) = cur[i];
+        for (int i = 0; i < kRaw; ++i)
+            *reinterpret_cast<u32x4*>(region + P::in_pad(4 * lane + 256 * i)) = cur[i];
         wave_lds_sync();
 
-        // ---- step 1: DFT16 over j of x[t + 64 j], t = 16c + n ----
-        cpx y[4][4];
+        // ---- step 1: block b = (transform f, column block c): DFT16 over j ----
+        cpx y[kB][4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            u32x4 b;
+        for (int b = 0; b < kB; ++b) {
+            const int base = (b / C) * N + 16 * (b % C) + n;
+            u32x4 x;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) b[e] = region[in_pad(16 * c + n + 64 * (4 * q + e))];
-            dft16_block(a, as_f16x8(b), y[c]);
+            for (int e = 0; e < 4; ++e) x[e] = region[P::in_pad(base + P::kM * (4 * q + e))];
+            dft16_block(a, as_f16x8(x), y[b]);
         }
-        // ---- steps 2-4: twiddle, DFT4 over c, twiddle ----
+        // ---- steps 2-4: twiddle, DFT_C over c, twiddle ----
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            cpx v[4];
+        for (int f = 0; f < P::kFPW; ++f)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) v[c] = cmul(y[c][r], w1[(c * 4 + r) * 64 + lane]);
-            Dft<4, FWD>::run(v);
-            y[0][r] = v[0];
+            for (int r = 0; r < 4; ++r) {
+                cpx v[C];
 #pragma unroll
-            for (int m = 1; m < 4; ++m) y[m][r] = cmul(v[m], w2[m - 1]);
-        }
-        // ---- step 5: transpose to (column block m, column k1, rows n) ----
-        // Row R = 16 m + k1 holds the 16 inputs n of sequence (k1, m); its
-        // 4-value chunks are rotated by k1/4 so reads and writes are
-        // bank-conflict free.
+                for (int c = 0; c < C; ++c) v[c] = cmul(y[f * C + c][r], w1[(c * 4 + r) * 64 + lane]);
+                Dft<C, FWD>::run(v);
+                y[f * C][r] = v[0];
+#pragma unroll
+                for (int m = 1; m < C; ++m) y[f * C + m][r] = cmul(v[m], w2[m - 1]);
+            }
+        // ---- step 5: transpose: row 16b + k1 holds the 16 inputs n of
+        // sequence (k1, m) of block b = (f, m); its 4-value chunks are rotated
+        // by k1/4 so reads and writes are bank-conflict free ----
         wave_lds_sync();
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (int b = 0; b < kB; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int k1 = q + 4 * r;
-                region[(16 * m + k1) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] = pack_half2(y[m][r]);
+                region[(16 * b + k1) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] = pack_half2(y[b][r]);
             }
         wave_lds_sync();
         // ---- step 6: DFT16 over n ----
-        cpx z[4][4];
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const u32x4 b = *reinterpret_cast<const u32x4*>(
-                region + (16 * m + n) * 16 + 4 * ((q + (n >> 2)) & 3));
-            dft16_block(a, as_f16x8(b), z[m]);
+        for (int b = 0; b < kB; ++b) {
+            const u32x4 x = *reinterpret_cast<const u32x4*>(
+                region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+            dft16_block(a, as_f16x8(x), y[b]);
         }
-        // ---- store: lane (n = k1, q) holds X[k1 + 16 m + 64 (q + 4 r)] ----
+        // ---- store: lane (n = k1, q), block (f, m) holds X_f[k1 + 16 m + 16C (q + 4 r)] ----
         wave_lds_sync();
 #pragma unroll
-        for (int m = 0; m < 4; ++m)
+        for (int b = 0; b < kB; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                region[out_pad(n + 16 * m + 64 * (q + 4 * r))] = pack_half2(z[m][r]);
+                region[P::out_pad((b / C) * N + n + 16 * (b % C) + P::kM * (q + 4 * r))] =
+                    pack_half2(y[b][r]);
         wave_lds_sync();
-        if (tile * P::kFPB + wave < batch) {
-            __half2* dst = out + (tile * P::kFPB + wave) * P::N;
+        const int nv = valid(tile);
+        __half2* dst = out + (tile * P::kFPB + wave * P::kFPW) * N;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                st_nt(reinterpret_cast<u32x4*>(dst + 4 * lane + 256 * i),
-                      *reinterpret_cast<const u32x4*>(region + out_pad(4 * lane + 256 * i)));
+        for (int i = 0; i < kRaw; ++i) {
+            const int e = 4 * lane + 256 * i;
+            if (e < nv)
+                st_nt(reinterpret_cast<u32x4*>(dst + e),
+                      *reinterpret_cast<const u32x4*>(region + P::out_pad(e)));
         }
     }
 }

@@ -6,6 +6,8 @@
 #include "thunderfft/detail/fft_mfma.hpp"
 #include "launch.hpp"
 
+#include <type_traits>
+
 #ifndef THFF_N
 #error "compile with -DTHFF_N=<transform length>"
 #endif
@@ -24,25 +26,38 @@ template <int N>
 constexpr LaunchShape launch_shape(int precision) {
     if (precision == 0) return N == 2048 ? LaunchShape{2, true} : LaunchShape{1, false};
     if (N <= 128) return {1, false};
-    if (N <= 512) return {2, false};
-    return {2, true};  // N = 1024 runs the MFMA kernel
+    if (N == 2048) return {4, true};  // N = 256 ... 2048 run the MFMA kernel
+    return {2, N == 1024};
 }
 
+// half2 lengths whose radix-16 stages run on MFMA (fft_mfma.hpp): N = 256*C.
+template <int N>
+inline constexpr bool kHalfOnMfma = N >= 256 && N <= 2048;
+
+// Only the launch shape in use is instantiated.
 template <class IO, int N, bool FWD>
-void enqueue(const LaunchShape& shape, unsigned grid, const IO* x, IO* y, int batch,
-             const float2* tw, int tpb, hipStream_t stream) {
-    if (shape.prefetch)
-        c2c_kernel<IO, N, FWD, true><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
-    else
-        c2c_kernel<IO, N, FWD, false><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
+void enqueue(unsigned grid, const IO* x, IO* y, int batch, const float2* tw, int tpb,
+             hipStream_t stream) {
+    constexpr bool kPf = launch_shape<N>(std::is_same_v<IO, float2> ? 0 : 1).prefetch;
+    c2c_kernel<IO, N, FWD, kPf><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
+}
+
+template <int N, bool FWD>
+void enqueue_mfma(unsigned grid, const __half2* x, __half2* y, int batch, const float2* tw,
+                  int tpb, hipStream_t stream) {
+    constexpr bool kPf = launch_shape<N>(1).prefetch;
+    c2c_mfma_kernel<N / 256, FWD, kPf><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
 }
 
 template <int N>
 hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, int batch,
                       const float2* tw, int num_cus, hipStream_t stream) {
-    using P = C2CPlan<N>;
     const LaunchShape shape = launch_shape<N>(precision);
-    const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
+    const bool mfma = precision != 0 && kHalfOnMfma<N>;
+    long long fpb = C2CPlan<N>::kFPB;
+    if constexpr (kHalfOnMfma<N>)
+        if (mfma) fpb = MfmaPlan<N / 256>::kFPB;
+    const long long ntiles = (static_cast<long long>(batch) + fpb - 1) / fpb;
     // Small batches spread one tile per workgroup over the whole device.
     const int tpb = ntiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? shape.tiles : 1;
     const unsigned grid = static_cast<unsigned>((ntiles + tpb - 1) / tpb);
@@ -50,22 +65,21 @@ hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, in
         const auto* x = static_cast<const float2*>(in);
         auto* y = static_cast<float2*>(out);
         if (forward)
-            enqueue<float2, N, true>(shape, grid, x, y, batch, tw, tpb, stream);
+            enqueue<float2, N, true>(grid, x, y, batch, tw, tpb, stream);
         else
-            enqueue<float2, N, false>(shape, grid, x, y, batch, tw, tpb, stream);
+            enqueue<float2, N, false>(grid, x, y, batch, tw, tpb, stream);
     } else {
         const auto* x = static_cast<const __half2*>(in);
         auto* y = static_cast<__half2*>(out);
-        if constexpr (N == 1024) {
-            // radix-16 stages on MFMA (fft_mfma.hpp); same tile size as c2c_kernel
+        if constexpr (kHalfOnMfma<N>) {
             if (forward)
-                c2c_mfma1024_kernel<true, true><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
+                enqueue_mfma<N, true>(grid, x, y, batch, tw, tpb, stream);
             else
-                c2c_mfma1024_kernel<false, true><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
+                enqueue_mfma<N, false>(grid, x, y, batch, tw, tpb, stream);
         } else if (forward) {
-            enqueue<__half2, N, true>(shape, grid, x, y, batch, tw, tpb, stream);
+            enqueue<__half2, N, true>(grid, x, y, batch, tw, tpb, stream);
         } else {
-            enqueue<__half2, N, false>(shape, grid, x, y, batch, tw, tpb, stream);
+            enqueue<__half2, N, false>(grid, x, y, batch, tw, tpb, stream);
         }
     }
     return hipGetLastError();
