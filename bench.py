@@ -148,6 +148,57 @@ def time_conv(kind: str, T: str, steps: int, warmup: int) -> dict:
             "bytes_per_call": nbytes}
 
 
+def compute_differential(T: str, repeats: int = 1000, trials: int = 3) -> dict:
+    """Reference-style compute time of the N=1024, batch-65536 transform
+    (sample/bench/paper_fft.cu:131-148): one launch loads every tile once,
+    repeats the transform R times in registers/LDS and stores once;
+    (t(2R) - t(R)) / R is one pass over the batch without HBM traffic.  The
+    reference publishes 126.53 us for fp32 (TF32) on A100 (README.md:72-76)."""
+    import ctypes
+
+    import torch
+
+    import thunderfft_amd as thff
+
+    path = os.path.join(ROOT, "thunderfft_amd", "_build", "libthff_bench_compute.so")
+    L = ctypes.CDLL(path)
+    L.thffx_compute_repeat.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    n, batch = N_FFT, BATCH
+    dt = torch.float32 if T == "float" else torch.float16
+    x = torch.empty(2 * n * batch, dtype=dt, device="cuda")
+    y = torch.empty_like(x)
+    stream = torch.cuda.current_stream()
+    thff.fill_uniform(T, x, n * batch, 0x7F4A7C15 + n, 0, stream)
+    x.mul_(1.0 / 32.0)  # keeps the repeated values finite a little longer
+    thff.ThunderFFTInitialize(T, n)
+    prec = 0 if T == "float" else 1
+
+    def once(r):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        rc = L.thffx_compute_repeat(prec, x.data_ptr(), y.data_ptr(), batch, r, stream.cuda_stream)
+        e.record(stream)
+        torch.cuda.synchronize()
+        if rc != 0:
+            raise RuntimeError(f"thffx_compute_repeat failed ({rc})")
+        return s.elapsed_time(e) * 1e3
+
+    for _ in range(3):
+        once(repeats)
+    per = []
+    for _ in range(trials):
+        t_r, t_2r = once(repeats), once(2 * repeats)
+        per.append((t_2r - t_r) / repeats)
+    thff.ThunderFFTFinalize(T)
+    del x, y
+    per.sort()
+    return {"precision": T, "repeats": repeats, "trials": trials,
+            "compute_us_per_pass": per[len(per) // 2],
+            "kernel": "fp32 VALU passes" if T == "float" else "fp16 MFMA (v_mfma_f32_16x16x32_f16)",
+            "reference_a100_us": 126.53 if T == "float" else None}
+
+
 def copy_bandwidth() -> float:
     """Device-to-device copy of a 512 MiB buffer (read + write), GB/s."""
     import torch
@@ -247,6 +298,11 @@ def main():
         print(f"[bench] {r['workload']}: {r['us_per_call']:.1f} us, {r['gbps']:.0f} GB/s "
               f"({r['pct_hbm_peak']:.1f}% of HBM peak), {r['gflops']:.0f} GFLOP/s",
               file=sys.stderr, flush=True)
+    for T in ("float", "half"):
+        r = compute_differential(T)
+        runs[f"compute_{T}"] = r
+        print(f"[bench] {T} N=1024 x 65536 differential compute (R={r['repeats']}): "
+              f"{r['compute_us_per_pass']:.1f} us per pass", file=sys.stderr, flush=True)
     copy_gbps = copy_bandwidth()
     main_run = runs["float_fwd"]
     cpu = None if a.no_cpu else cpu_baseline(a.cpu_seconds)

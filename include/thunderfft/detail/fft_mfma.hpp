@@ -122,6 +122,86 @@ struct MfmaPlan {
     }
 };
 
+// Per-lane DFT16 operands, the step-2 twiddles W_N^(t*k1) (t = 16c + n,
+// k1 = q + 4r; shared by the workgroup through LDS, w1 = [c][r][lane]) and the
+// step-4 twiddles W_16C^(n*m) = W_N^(16 n m) (registers), all from the
+// positive-angle table and conjugated here for the forward direction.
+// Collective over the 256-lane workgroup (ends with a barrier).
+template <int C, bool FWD>
+__device__ __forceinline__ void mfma_setup(f16x8 (&a)[2][2], cpx* w1, cpx* w2,
+                                           const float2* __restrict__ tw) {
+    using P = MfmaPlan<C>;
+    constexpr int N = P::N;
+    const int tid = threadIdx.x, lane = tid & 63, n = lane & 15;
+    dft16_operands<FWD>(a, lane);
+    for (int e = tid; e < P::kTw1; e += 256) {
+        const int l = e & 63, r = (e >> 6) & 3, c = e >> 8;
+        const float2 x = tw[((16 * c + (l & 15)) * ((l >> 4) + 4 * r)) & (N - 1)];
+        w1[e] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+    }
+#pragma unroll
+    for (int m = 1; m < C; ++m) {
+        const float2 x = tw[(16 * n * m) & (N - 1)];
+        w2[m - 1] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+    }
+    __syncthreads();
+}
+
+// Steps 1-6 for the kFPW transforms a wave has staged in `region` (natural
+// order at MfmaPlan<C>::in_pad positions); on return lane (n = k1, q) holds,
+// for block b = (f, m), y[b][r] = X_f[k1 + 16 m + 16C (q + 4 r)].  `region`
+// is overwritten (the transpose of step 5).
+template <int C, bool FWD>
+__device__ __forceinline__ void mfma_fft_staged(unsigned* region, const f16x8 (&a)[2][2],
+                                                const cpx* w1, const cpx* w2, int lane,
+                                                cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
+    using P = MfmaPlan<C>;
+    constexpr int N = P::N;
+    constexpr int kB = P::kBlocks;
+    const int n = lane & 15, q = lane >> 4;
+    // ---- step 1: block b = (transform f, column block c): DFT16 over j ----
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+        const int base = (b / C) * N + 16 * (b % C) + n;
+        u32x4 x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = region[P::in_pad(base + P::kM * (4 * q + e))];
+        dft16_block(a, as_f16x8(x), y[b]);
+    }
+    // ---- steps 2-4: twiddle, DFT_C over c, twiddle ----
+#pragma unroll
+    for (int f = 0; f < P::kFPW; ++f)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            cpx v[C];
+#pragma unroll
+            for (int c = 0; c < C; ++c) v[c] = cmul(y[f * C + c][r], w1[(c * 4 + r) * 64 + lane]);
+            Dft<C, FWD>::run(v);
+            y[f * C][r] = v[0];
+#pragma unroll
+            for (int m = 1; m < C; ++m) y[f * C + m][r] = cmul(v[m], w2[m - 1]);
+        }
+    // ---- step 5: transpose: row 16b + k1 holds the 16 inputs n of
+    // sequence (k1, m) of block b = (f, m); its 4-value chunks are rotated
+    // by k1/4 so reads and writes are bank-conflict free ----
+    wave_lds_sync();
+#pragma unroll
+    for (int b = 0; b < kB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int k1 = q + 4 * r;
+            region[(16 * b + k1) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] = pack_half2(y[b][r]);
+        }
+    wave_lds_sync();
+    // ---- step 6: DFT16 over n ----
+#pragma unroll
+    for (int b = 0; b < kB; ++b) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(
+            region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+        dft16_block(a, as_f16x8(x), y[b]);
+    }
+}
+
 // Batched C2C of half2 signals of N = 256*C on MFMA (C = 4 is N = 1024 as
 // described at the top of this file; in general N = 16 x (C x 16)):
 //   1. DFT16 over j of x[t + 16C j] for the 16C sequences t = 16c + n
@@ -152,22 +232,8 @@ c2c_mfma_kernel(const __half2* __restrict__ in,
     unsigned* region = lds + wave * P::kRegion;
 
     f16x8 a[2][2];
-    dft16_operands<FWD>(a, lane);
-    // Step-2 twiddles W_N^(t*k1), t = 16c + n, k1 = q + 4r, shared through
-    // LDS; step-4 twiddles W_16C^(n*m) = W_N^(16 n m); both from the
-    // positive-angle table, conjugated here for the forward direction.
-    for (int e = tid; e < P::kTw1; e += 256) {
-        const int l = e & 63, r = (e >> 6) & 3, c = e >> 8;
-        const float2 x = tw[((16 * c + (l & 15)) * ((l >> 4) + 4 * r)) & (N - 1)];
-        w1[e] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
-    }
     cpx w2[C > 1 ? C - 1 : 1];
-#pragma unroll
-    for (int m = 1; m < C; ++m) {
-        const float2 x = tw[(16 * n * m) & (N - 1)];
-        w2[m - 1] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
-    }
-    __syncthreads();
+    mfma_setup<C, FWD>(a, w1, w2, tw);
 
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
     long long tile = static_cast<long long>(blockIdx.x) * tiles_per_block;
@@ -208,48 +274,8 @@ c2c_mfma_kernel(const __half2* __restrict__ in,
             *reinterpret_cast<u32x4*>(region + P::in_pad(4 * lane + 256 * i)) = cur[i];
         wave_lds_sync();
 
-        // ---- step 1: block b = (transform f, column block c): DFT16 over j ----
         cpx y[kB][4];
-#pragma unroll
-        for (int b = 0; b < kB; ++b) {
-            const int base = (b / C) * N + 16 * (b % C) + n;
-            u32x4 x;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) x[e] = region[P::in_pad(base + P::kM * (4 * q + e))];
-            dft16_block(a, as_f16x8(x), y[b]);
-        }
-        // ---- steps 2-4: twiddle, DFT_C over c, twiddle ----
-#pragma unroll
-        for (int f = 0; f < P::kFPW; ++f)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                cpx v[C];
-#pragma unroll
-                for (int c = 0; c < C; ++c) v[c] = cmul(y[f * C + c][r], w1[(c * 4 + r) * 64 + lane]);
-                Dft<C, FWD>::run(v);
-                y[f * C][r] = v[0];
-#pragma unroll
-                for (int m = 1; m < C; ++m) y[f * C + m][r] = cmul(v[m], w2[m - 1]);
-            }
-        // ---- step 5: transpose: row 16b + k1 holds the 16 inputs n of
-        // sequence (k1, m) of block b = (f, m); its 4-value chunks are rotated
-        // by k1/4 so reads and writes are bank-conflict free ----
-        wave_lds_sync();
-#pragma unroll
-        for (int b = 0; b < kB; ++b)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int k1 = q + 4 * r;
-                region[(16 * b + k1) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] = pack_half2(y[b][r]);
-            }
-        wave_lds_sync();
-        // ---- step 6: DFT16 over n ----
-#pragma unroll
-        for (int b = 0; b < kB; ++b) {
-            const u32x4 x = *reinterpret_cast<const u32x4*>(
-                region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
-            dft16_block(a, as_f16x8(x), y[b]);
-        }
+        mfma_fft_staged<C, FWD>(region, a, w1, w2, lane, y);
         // ---- store: lane (n = k1, q), block (f, m) holds X_f[k1 + 16 m + 16C (q + 4 r)] ----
         wave_lds_sync();
 #pragma unroll

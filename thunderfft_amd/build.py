@@ -91,7 +91,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
 
 APPS = ("thff_validate",)
 # Shared libraries of kernels written against the public device API (tests use them).
-DEVICE_EXAMPLES = ("device_example",)
+DEVICE_EXAMPLES = ("device_example", "bench_compute")
 
 
 def build_apps(verbose: bool = False) -> list[str]:
