@@ -218,3 +218,30 @@ def test_config2_n1024_float(batch):
 def test_config3_sweep(T, n):
     """batch = 2^26 / N complex values per buffer."""
     _large_case(T, n, (1 << 26) // n)
+
+
+@pytest.mark.parametrize("mode", ["quick", "full"])
+def test_thff_validate_matrix(mode, tmp_path):
+    """The thff_validate program (the reference's sample/validation/
+    fft_validation.cu matrix): direct (device API) and public paths, every
+    length, both precisions and directions, the four input kinds and tail
+    batches, against hipFFT Z2Z fp64; exit status 0 and every CSV row passes."""
+    import csv
+    import subprocess
+
+    exe = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                       "thunderfft_amd", "_build", "thff_validate")
+    out = tmp_path / "validate.csv"
+    args = [exe, "--csv", str(out)] + (["--quick"] if mode == "quick" else [])
+    res = subprocess.run(args, capture_output=True, text=True, timeout=600)
+    print(res.stderr[-2000:], flush=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    rows = list(csv.DictReader(open(out)))
+    assert len(rows) == (88 if mode == "quick" else 532)
+    assert all(r["pass"] == "1" for r in rows)
+    worst = {}
+    for r in rows:
+        k = r["precision"]
+        worst[k] = max(worst.get(k, 0.0), float(r["relative_l2"]))
+    print("worst relative L2 per precision:", worst, flush=True)
+    assert worst["fp32"] <= TIGHT["float"] and worst["fp16"] <= TIGHT["half"]

@@ -100,9 +100,8 @@ def build_apps(verbose: bool = False) -> list[str]:
     out = []
     for app in APPS:
         exe = os.path.join(BUILD, app)
-        cmd = [cc, "-std=c++17", "-O2", "-I", os.path.join(ROOT, "include"),
-               os.path.join(PKG, "apps", app + ".cpp"), "-o", exe, "-L", PKG, "-lthunderfft_amd",
-               "-Wl,-rpath,$ORIGIN/.."]
+        cmd = [cc, *common_flags(), os.path.join(PKG, "apps", app + ".hip"), "-o", exe,
+               "-L", PKG, "-lthunderfft_amd", "-lhipfft", "-Wl,-rpath,$ORIGIN/.."]
         if verbose:
             print(" ".join(cmd), flush=True)
         res = subprocess.run(cmd, capture_output=True, text=True)
