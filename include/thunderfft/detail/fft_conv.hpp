@@ -158,4 +158,179 @@ __global__ __launch_bounds__(256) void conv2d64_kernel(const IO* __restrict__ x,
     }
 }
 
+// ---------------------------------------------------------------------------
+// Real-input, real-output fused convolution with one real filter per channel
+// (the reference's thunder_convN_block_kernel_realin_realout,
+// sample/conv1d/conv1d_fullfft_l4096_thunder.cu:280-331, generalised to all
+// seven lengths and both storage types):
+//   y[b][d] = IFFT(FFT(x[b][d]) * H[d])   (length N), x, y real [batch][D][N].
+// Because h is real, two signals of one channel share a complex transform:
+// z = x[2p][d] + i x[2p+1][d] gives z (*) h = x[2p][d] (*) h + i x[2p+1][d] (*) h,
+// so complex transform tau = p*D + d carries both, and the real and
+// imaginary parts of its result are the two outputs.  The filter spectra
+// H[d][k] = scale * FFT(h[d])[k] (fp32 complex, natural order) are prepared
+// once by conv1d_real_filter_kernel; the convolution kernel then writes
+// IFFT(FFT(x) * H) unnormalized, which with scale = 1 is N * (x (*) h), the
+// reference's output, and with scale = 1/N is x (*) h itself.  The pairing
+// needs H[d] to be Hermitian (H[k] = conj H[N - k]), which every spectrum of a
+// real filter is.
+// ---------------------------------------------------------------------------
+
+// Real scalars of one storage type: 16-byte vectors of kVec values.
+template <class IO>
+struct RealIo;
+template <>
+struct RealIo<float2> {
+    using S = float;
+    static constexpr int kVec = 4;
+    __device__ __forceinline__ static void decode(u32x4 w, float* v) {
+        v[0] = as_f32(w.x), v[1] = as_f32(w.y), v[2] = as_f32(w.z), v[3] = as_f32(w.w);
+    }
+    __device__ __forceinline__ static u32x4 encode(const float* v) {
+        return u32x4{as_u32(v[0]), as_u32(v[1]), as_u32(v[2]), as_u32(v[3])};
+    }
+};
+template <>
+struct RealIo<__half2> {
+    using S = __half;
+    static constexpr int kVec = 8;
+    __device__ __forceinline__ static void decode(u32x4 w, float* v) {
+        const unsigned u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float2 f = __half22float2(__builtin_bit_cast(__half2, u[i]));
+            v[2 * i] = f.x, v[2 * i + 1] = f.y;
+        }
+    }
+    __device__ __forceinline__ static u32x4 encode(const float* v) {
+        unsigned u[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            u[i] = __builtin_bit_cast(unsigned, __floats2half2_rn(v[2 * i], v[2 * i + 1]));
+        return u32x4{u[0], u[1], u[2], u[3]};
+    }
+};
+
+// H[d][k] = scale * FFT(h[d])[k] for `channels` real fp32 filters h[d] of N
+// taps (fp32 for both storage types, so half convolutions keep exact taps).
+template <int N>
+__global__ __launch_bounds__(256) void conv1d_real_filter_kernel(const float* __restrict__ h,
+                                                                 float2* __restrict__ spectrum,
+                                                                 int channels, float scale,
+                                                                 const float2* __restrict__ tw) {
+    using P = C2CPlan<N>;
+    __shared__ cpx lds[P::kLdsSlots];
+    const int tid = threadIdx.x, f = tid / P::kTPF, t = tid % P::kTPF;
+    cpx* slot = lds + f * P::kSlot;
+    LaneTwiddles<N> w;
+    w.load(t, tw);
+    const long long d = static_cast<long long>(blockIdx.x) * P::kFPB + f;
+    const bool ok = d < channels;
+    cpx v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        v[j] = {ok ? h[d * N + t + j * P::kTPF] : 0.f, 0.f};
+    }
+    fft_registers<N, true>(v, slot, t, w);
+    if (ok) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            spectrum[d * N + t + j * P::kTPF] = make_float2(v[j].re * scale, v[j].im * scale);
+    }
+}
+
+template <class IO, int N>
+__global__ __launch_bounds__(256) void conv1d_real_kernel(
+    const typename RealIo<IO>::S* __restrict__ x, const float2* __restrict__ spectrum,
+    typename RealIo<IO>::S* __restrict__ y, int batch, int channels,
+    const float2* __restrict__ tw, int tiles_per_block) {
+    using P = C2CPlan<N>;
+    using R = RealIo<IO>;
+    constexpr int kVec = R::kVec;
+    // A tile is kFPB complex transforms = 4096 complex values; value e
+    // (transform e / N, element e % N) is staged at LDS position lds_pad(e),
+    // which is where the transform's slot expects it.  Wave w moves values
+    // [1024 w, 1024 (w + 1)), which for N <= 1024 are exactly the transforms
+    // its own lanes compute; lane l takes kVec of them per step, from the
+    // same offset of both rows of a pair.
+    constexpr int kSteps = 1024 / (64 * kVec);
+    __shared__ cpx lds[P::kLdsSlots];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int f = tid / P::kTPF, t = tid % P::kTPF;
+    cpx* slot = lds + f * P::kSlot;
+    LaneTwiddles<N> w;
+    w.load(t, tw);
+
+    const long long pairs = (static_cast<long long>(batch) + 1) / 2;
+    const long long transforms = pairs * channels;
+    const long long ntiles = (transforms + P::kFPB - 1) / P::kFPB;
+    long long tile, tile_end;
+    block_tiles(ntiles, tiles_per_block, tile, tile_end);
+
+    for (; tile < tile_end; ++tile) {
+        // ---- both rows of each transform -> LDS as (re, im) = (row 0, row 1) ----
+        long long base0[kSteps], base1[kSteps];  // element offsets, -1 = no row
+#pragma unroll
+        for (int i = 0; i < kSteps; ++i) {
+            const int e = 1024 * wave + kVec * lane + 64 * kVec * i;
+            const long long tau = tile * P::kFPB + e / N;
+            const long long p = tau / channels, d = tau - p * channels;
+            const long long b0 = 2 * p, b1 = b0 + 1;
+            const int n = e % N;
+            base0[i] = tau < transforms ? (b0 * channels + d) * N + n : -1;
+            base1[i] = tau < transforms && b1 < batch ? (b1 * channels + d) * N + n : -1;
+        }
+        u32x4 r0[kSteps], r1[kSteps];
+#pragma unroll
+        for (int i = 0; i < kSteps; ++i) {
+            r0[i] = base0[i] >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + base0[i])) : u32x4{};
+            r1[i] = base1[i] >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + base1[i])) : u32x4{};
+        }
+        region_sync<P::kWaveLocal>();
+#pragma unroll
+        for (int i = 0; i < kSteps; ++i) {
+            const int e = 1024 * wave + kVec * lane + 64 * kVec * i;
+            float a[kVec], b[kVec];
+            R::decode(r0[i], a);
+            R::decode(r1[i], b);
+#pragma unroll
+            for (int c = 0; c < kVec; ++c) lds[lds_pad(e + c)] = cpx{a[c], b[c]};
+        }
+        region_sync<P::kWaveLocal>();
+        cpx v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = slot[lds_pad(t + j * P::kTPF)];
+
+        // ---- FFT, product with the channel's spectrum, inverse FFT ----
+        const long long tau = tile * P::kFPB + f;
+        const long long d = tau < transforms ? tau % channels : 0;
+        const float2* hs = spectrum + d * N + t;
+        fft_registers<N, true>(v, slot, t, w);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const float2 hk = hs[j * P::kTPF];
+            v[j] = cmul(v[j], cpx{hk.x, hk.y});
+        }
+        fft_registers<N, false>(v, slot, t, w);
+
+        // ---- real part -> row 0, imaginary part -> row 1 ----
+        region_sync<P::kWaveLocal>();
+#pragma unroll
+        for (int j = 0; j < 16; ++j) slot[lds_pad(t + j * P::kTPF)] = v[j];
+        region_sync<P::kWaveLocal>();
+#pragma unroll
+        for (int i = 0; i < kSteps; ++i) {
+            const int e = 1024 * wave + kVec * lane + 64 * kVec * i;
+            float a[kVec], b[kVec];
+#pragma unroll
+            for (int c = 0; c < kVec; ++c) {
+                const cpx z = lds[lds_pad(e + c)];
+                a[c] = z.re, b[c] = z.im;
+            }
+            if (base0[i] >= 0) st_nt(reinterpret_cast<u32x4*>(y + base0[i]), R::encode(a));
+            if (base1[i] >= 0) st_nt(reinterpret_cast<u32x4*>(y + base1[i]), R::encode(b));
+        }
+    }
+}
+
 }  // namespace thff

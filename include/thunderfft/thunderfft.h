@@ -96,6 +96,44 @@ int thff_conv1d(int precision, int n, const void* d_x, const void* d_h, void* d_
 int thff_conv1d_async(int precision, int n, const void* d_x, const void* d_h, void* d_y,
                       int batch, int per_signal_filter, void* stream);
 
+/* Spectra of `channels` real filters for thff_conv1d_real: for every channel
+ * d, spectrum[d][k] = scale * FFT(h[d])[k], k < n, as fp32 complex (8 bytes per
+ * value, natural order).  h holds channels*n real fp32 taps, zero-padded to n,
+ * for both precisions; `precision` names the convolution the spectra are for
+ * (its twiddle table is used).  Replaces the reference's filter-spectrum
+ * preparation filter_fft_once (cuFFT C2C + f32_to_h2 + permute_filter_layout*,
+ * sample/conv1d/conv1d_fullfft_l4096_thunder.cu:475-497,154-226); scale = 1
+ * gives its spectra, scale = 1/n folds the inverse's normalisation in.
+ * Requires thff_initialize(precision, n); THFF_EINVAL for a bad precision or
+ * length, channels < 0, null or aliased pointers; channels = 0 is a no-op.
+ * Synchronises `stream` before returning. */
+int thff_conv1d_real_filter(int precision, int n, const void* d_h, void* d_spectrum,
+                            int channels, float scale, void* stream);
+
+/* thff_conv1d_real_filter without the final stream synchronisation. */
+int thff_conv1d_real_filter_async(int precision, int n, const void* d_h, void* d_spectrum,
+                                  int channels, float scale, void* stream);
+
+/* Fused real-input, real-output convolution with one filter per channel (the
+ * reference's thunder_convN_block_kernel_realin_realout,
+ * sample/conv1d/conv1d_fullfft_l4096_thunder.cu:280-331, launched by run_case
+ * :508-515; the reference instantiates n = 256, 1024, 4096 in half, this
+ * takes all seven lengths in float or half):
+ *   y[b][d] = Re IFFT(FFT(x[b][d]) * spectrum[d])   (unnormalized inverse),
+ * x and y real [batch][channels][n] in `precision` storage, spectrum from
+ * thff_conv1d_real_filter(precision, n, ...) for the same channels.  With
+ * scale = 1 the output is n * (x (*) h), as the reference writes it; with
+ * scale = 1/n it is the circular convolution x (*) h.  x and y must be
+ * 16-byte aligned.  Same checks and return codes as thff_conv1d (y may alias
+ * neither x nor spectrum; channels <= 0 is THFF_EINVAL when batch > 0).
+ * Synchronises `stream` before returning. */
+int thff_conv1d_real(int precision, int n, const void* d_x, const void* d_spectrum, void* d_y,
+                     int batch, int channels, void* stream);
+
+/* thff_conv1d_real without the final stream synchronisation. */
+int thff_conv1d_real_async(int precision, int n, const void* d_x, const void* d_spectrum,
+                           void* d_y, int batch, int channels, void* stream);
+
 /* Fused 2-D circular convolution of `batch` rows x cols row-major images with
  * one shared rows x cols filter (no function counterpart in the reference
  * library; the reference's 2-D convolution is the sample

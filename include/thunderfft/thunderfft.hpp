@@ -111,6 +111,30 @@ inline void ThunderFFT_conv1d(const vec2_t<T>* d_x, const vec2_t<T>* d_h, vec2_t
                               per_signal_filter ? 1 : 0, static_cast<void*>(stream)));
 }
 
+// Spectra of `channels` real fp32 filters h[d] (N taps each) for
+// ThunderFFT_conv1d_real<T, N>: spectrum[d][k] = scale * FFT(h[d])[k], fp32
+// complex.  Replaces the reference's filter_fft_once
+// (sample/conv1d/conv1d_fullfft_l4096_thunder.cu:475-497); Initialize<T>(N) first.
+template <typename T, int N>
+inline void ThunderFFT_conv1d_real_filter(const float* d_h, float2* d_spectrum, int channels,
+                                          float scale = 1.0f, hipStream_t stream = 0) {
+    static_assert(is_supported_length<N>, "Unsupported ThunderFFT length");
+    detail::check(thff_conv1d_real_filter(detail::precision_code<T>(), N, d_h, d_spectrum,
+                                          channels, scale, static_cast<void*>(stream)));
+}
+
+// Fused real convolution of x[batch][channels][N] with one filter per channel:
+// y[b][d] = Re IFFT(FFT(x[b][d]) * spectrum[d]), unnormalized (the reference's
+// thunder_convN_block_kernel_realin_realout,
+// sample/conv1d/conv1d_fullfft_l4096_thunder.cu:280-331).
+template <typename T, int N>
+inline void ThunderFFT_conv1d_real(const T* d_x, const float2* d_spectrum, T* d_y, int batch,
+                                   int channels, hipStream_t stream = 0) {
+    static_assert(is_supported_length<N>, "Unsupported ThunderFFT length");
+    detail::check(thff_conv1d_real(detail::precision_code<T>(), N, d_x, d_spectrum, d_y, batch,
+                                   channels, static_cast<void*>(stream)));
+}
+
 // Fused 2-D circular convolution of `batch` Rows x Cols images with one shared
 // filter: y[b] = IFFT2(FFT2(x[b]) * FFT2(h)) / (Rows*Cols).  Rows = Cols = 64;
 // Initialize<T>(64) first.  No counterpart in the reference's library API

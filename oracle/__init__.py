@@ -58,6 +58,10 @@ def lib():
         L.thff_make_input_gaussian.argtypes = [ctypes.c_int, ctypes.c_long, fp]
         L.thff_circconv1d_f64.argtypes = [ctypes.c_int, ctypes.c_long, ctypes.c_int, dp, dp, dp]
         L.thff_circconv2d_f64.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_long, dp, dp, dp]
+        L.thff_circconv1d_channels_f64.argtypes = [ctypes.c_int, ctypes.c_long, ctypes.c_int,
+                                                   ctypes.c_int, dp, dp, dp]
+        L.thff_conv_real_inputs.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_long,
+                                            ctypes.c_int, ctypes.c_uint, fp, fp]
         _lib = L
     return _lib
 
@@ -190,3 +194,35 @@ def circconv2d(x, h) -> np.ndarray:
                                      _p(h.view(np.float64), ctypes.c_double),
                                      _p(out.view(np.float64), ctypes.c_double)), "circconv2d")
     return out
+
+
+def circconv1d_channels(x, h, taps: int | None = None) -> np.ndarray:
+    """Real direct circular convolution, one filter per channel (fp64).
+
+    x: real (..., channels, n) signals; h: real (channels, n) filters of which
+    the first ``taps`` (default n) are used.  conv1d_fullfft_l4096_thunder.cu:499-520.
+    """
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    h = np.ascontiguousarray(h, dtype=np.float64)
+    channels, n = h.shape
+    assert x.shape[-1] == n and x.shape[-2] == channels
+    taps = n if taps is None else taps
+    out = np.empty_like(x)
+    _check(lib().thff_circconv1d_channels_f64(n, x.size // n, channels, taps,
+                                              _p(x, ctypes.c_double), _p(h, ctypes.c_double),
+                                              _p(out, ctypes.c_double)), "circconv1d_channels")
+    return out
+
+
+def conv_real_inputs(n: int, taps: int, batch: int, channels: int, seed: int = 42):
+    """The real convolution sample's seeded inputs (srand(seed), rand()).
+
+    Returns x float32 (batch, channels, n) and h float32 (channels, n), taps
+    k >= ``taps`` zero.  conv1d_fullfft_l4096_thunder.cu:389-401, seed 42 at :617.
+    """
+    x = np.empty((batch, channels, n), dtype=np.float32)
+    h = np.empty((channels, n), dtype=np.float32)
+    _check(lib().thff_conv_real_inputs(n, taps, batch * channels, channels, seed,
+                                       _p(x, ctypes.c_float), _p(h, ctypes.c_float)),
+           "conv_real_inputs")
+    return x, h

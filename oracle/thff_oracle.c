@@ -28,7 +28,10 @@
  *     -> thff_uniform_fill (identical to the library's device generator)
  *   - direct circular convolution for the fused-convolution checks
  *     (conv1d_fullfft_l4096_thunder.cu:499-545) -> thff_circconv1d_f64,
- *     thff_circconv2d_f64
+ *     thff_circconv2d_f64, and its real per-channel form
+ *     thff_circconv1d_channels_f64
+ *   - the real convolution sample's seeded inputs (srand/rand,
+ *     conv1d_fullfft_l4096_thunder.cu:389-401) -> thff_conv_real_inputs
  *
  * Pinning: every function here is checked in tests/test_oracle.py against
  * closed forms (impulse/constant/tone spectra), invariants (Parseval,
@@ -478,5 +481,53 @@ int thff_circconv2d_f64(int rows, int cols, long batch, const double* x, const d
                 ys[2 * ((size_t)r * cols + c) + 1] = si;
             }
     }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Real-input convolution with one real filter per channel, as the real     */
+/* fused-convolution sample validates it (conv1d_fullfft_l4096_thunder.cu:  */
+/* 499-520): signals x[s][n], s = b*channels + d, filter d = s mod channels */
+/* with `taps` leading taps h[d][k], k < taps (the rest of its n are zero): */
+/*   y[s][n] = sum_{k < taps} x[s][(n - k) mod n] * h[d][k].                */
+/* ------------------------------------------------------------------------ */
+int thff_circconv1d_channels_f64(int n, long signals, int channels, int taps, const double* x,
+                                 const double* h, double* y) {
+    if (n <= 0 || signals < 0 || channels <= 0 || taps < 0 || taps > n) return -1;
+    for (long s = 0; s < signals; ++s) {
+        const double* xs = x + (size_t)s * n;
+        const double* hs = h + (size_t)(s % channels) * n;
+        double* ys = y + (size_t)s * n;
+        for (int k = 0; k < n; ++k) {
+            double acc = 0;
+            for (int j = 0; j < taps; ++j) {
+                int m = k - j;
+                if (m < 0) m += n;
+                acc += xs[m] * hs[j];
+            }
+            ys[k] = acc;
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* The real fused-convolution sample's inputs (conv1d_fullfft_l4096_thunder */
+/* .cu:389-401, seeded by std::srand(seed) at :617): after srand(seed),     */
+/* signals*n values rand()/RAND_MAX in signal order, then for each channel  */
+/* d its first `taps` taps (rand()/RAND_MAX)/n (the sample draws no         */
+/* imaginary part for its real filters).  Taps k >= taps are zero.  Uses    */
+/* the C library's own srand/rand, i.e. the same sequence as the sample on  */
+/* the same C library.                                                      */
+/* ------------------------------------------------------------------------ */
+int thff_conv_real_inputs(int n, int taps, long signals, int channels, unsigned seed, float* x,
+                          float* h) {
+    if (n <= 0 || signals < 0 || channels <= 0 || taps < 0 || taps > n) return -1;
+    srand(seed);
+    for (size_t i = 0; i < (size_t)signals * n; ++i) x[i] = (float)rand() / (float)RAND_MAX;
+    memset(h, 0, sizeof(float) * (size_t)channels * n);
+    for (int d = 0; d < channels; ++d)
+        for (int k = 0; k < taps; ++k)
+            h[(size_t)d * n + k] = ((float)rand() / (float)RAND_MAX) / (float)n;
     return 0;
 }

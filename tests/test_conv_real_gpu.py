@@ -1,0 +1,220 @@
+"""GPU parity of the real-input fused convolution (thff_conv1d_real) and its
+filter-spectrum preparation (thff_conv1d_real_filter), through the C ABI.
+
+The reference's thunder_convN_block_kernel_realin_realout
+(sample/conv1d/conv1d_fullfft_l4096_thunder.cu:280-331) convolves real half
+signals [B][D][N] with one real filter per channel and writes the
+unnormalized result; its driver (:354-570) draws the inputs with
+srand(42)/rand(), prepares the spectra once, and gates rel L2 of output/N
+against the direct circular convolution at 5e-3 (:499-554).  Here:
+
+* the reference's own cases (N = 256, 1024, 4096; its default K = 9, B = D = 1
+  and wider K, B, D) on its own seeded inputs, half and float;
+* every length x {float, half} with channel counts and odd batches that leave
+  partial tiles and an unpaired last signal, against the fp64 direct
+  convolution, with output sentinels;
+* the spectra against numpy's FFT;
+* at full size (65535 signals of 1024; 2112 of 4096) the exact property that a
+  unit impulse at tap s rolls each signal by s.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from thff_testlib import GATE, SIZES
+
+pytestmark = pytest.mark.gpu
+
+# float: two fp32 transforms and a product; half: plus one output rounding.
+TIGHT = {"float": 5e-6, "half": 1e-3}
+GUARD = 16
+GUARD_VALUE = -37.0
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    import torch
+
+    import thunderfft_amd as thff
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    thff.lib()
+    yield
+    thff.ThunderFFTFinalize("float")
+    thff.ThunderFFTFinalize("half")
+
+
+def represent(x, T):
+    """The real values storage type T holds (float32, or binary16 round trip)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if T == "float":
+        return x.copy()
+    return oracle.f16_bits_to_f32(oracle.f32_to_f16_bits(x.reshape(-1))).reshape(x.shape)
+
+
+def to_device(x, T):
+    import torch
+
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    if T == "float":
+        return torch.from_numpy(x.copy()).cuda()
+    bits = oracle.f32_to_f16_bits(x)
+    return torch.from_numpy(bits.view(np.int16).copy()).cuda().view(torch.float16)
+
+
+def from_device(t, T):
+    import torch
+
+    if T == "float":
+        return t.detach().cpu().numpy().astype(np.float32)
+    bits = t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+    return oracle.f16_bits_to_f32(bits)
+
+
+def spectra(T, n, h, scale):
+    """Device spectra of the real fp32 filters h (channels, n)."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    channels = h.shape[0]
+    d_h = torch.from_numpy(np.ascontiguousarray(h, dtype=np.float32).reshape(-1)).cuda()
+    d_s = torch.full((channels * n * 2,), float("nan"), dtype=torch.float32, device="cuda")
+    thff.ThunderFFTInitialize(T, n)
+    thff.ThunderFFT_conv1d_real_filter(T, n, d_h, d_s, channels, scale)
+    return d_s
+
+
+def convolve(T, n, x, d_spec, channels, sync=True):
+    """Run the fused real convolution on x (batch, channels, n); returns the
+    output (batch, channels, n) and the number of changed output sentinels."""
+    import thunderfft_amd as thff
+
+    batch = x.shape[0]
+    count = batch * channels * n
+    d_x = to_device(x, T)
+    host = np.full(count + GUARD, np.nan, dtype=np.float32)
+    host[count:] = GUARD_VALUE
+    d_y = to_device(host, T)
+    if sync:
+        thff.ThunderFFT_conv1d_real(T, n, d_x, d_spec, d_y, batch, channels)
+    else:
+        import torch
+
+        thff.ThunderFFT_conv1d_real_async(T, n, d_x, d_spec, d_y, batch, channels)
+        torch.cuda.synchronize()
+    y = from_device(d_y, T)
+    guards = int(np.sum(y[count:] != GUARD_VALUE))
+    return y[:count].reshape(batch, channels, n), guards
+
+
+def rel_l2(y, ref):
+    m = oracle.metrics(np.asarray(y, np.float32).astype(np.complex64),
+                       np.asarray(ref, np.float64).astype(np.complex128))
+    return m["rel_l2"], m["nonfinite"]
+
+
+# The reference's cases: its default (K = 9, B = D = 1, :575-585) and wider
+# K / B / D, including K = N and an odd B*D.
+REFERENCE_CASES = [(9, 1, 1), (1, 2, 3), (53, 3, 5), (None, 4, 16)]
+
+
+@pytest.mark.parametrize("T", ["half", "float"])
+@pytest.mark.parametrize("n", [256, 1024, 4096])
+def test_reference_cases_on_reference_inputs(T, n):
+    for taps, batch, channels in REFERENCE_CASES:
+        taps = n if taps is None else taps
+        x, h = oracle.conv_real_inputs(n, taps, batch, channels, seed=42)
+        xr = represent(x, T)
+        d_spec = spectra(T, n, h, 1.0)  # the reference's unscaled spectra
+        y, guards = convolve(T, n, xr, d_spec, channels)
+        ref = oracle.circconv1d_channels(xr, h, taps)
+        err, bad = rel_l2(y / n, ref)  # the reference's gate: output / N
+        label = f"{T} N={n} K={taps} B={batch} D={channels}: rel_l2(out/N)={err:.3e}"
+        print(label, flush=True)
+        assert bad == 0 and guards == 0, label
+        assert err <= GATE and err <= TIGHT[T], label
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("n", SIZES)
+def test_all_lengths_partial_tiles(T, n):
+    import thunderfft_amd as thff
+
+    fpb = thff.transforms_per_block(n)
+    rng = np.random.default_rng(n)
+    for channels, batch in ((1, 1), (3, 5), (fpb + 1, 2)):
+        if n >= 2048 and channels * batch > 12:
+            continue
+        x = rng.uniform(-1, 1, size=(batch, channels, n)).astype(np.float32)
+        h = rng.normal(0, 1 / np.sqrt(n), size=(channels, n)).astype(np.float32)
+        xr = represent(x, T)
+        d_spec = spectra(T, n, h, 1.0 / n)  # normalised: y = x (*) h
+        y, guards = convolve(T, n, xr, d_spec, channels)
+        ref = oracle.circconv1d_channels(xr, h)
+        err, bad = rel_l2(y, ref)
+        label = f"{T} N={n} D={channels} B={batch}: rel_l2={err:.3e}"
+        print(label, flush=True)
+        assert bad == 0 and guards == 0, label
+        assert err <= GATE and err <= TIGHT[T], label
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("n", SIZES)
+def test_filter_spectra_match_numpy(T, n):
+    rng = np.random.default_rng(3 * n)
+    channels = 5
+    h = rng.normal(size=(channels, n)).astype(np.float32)
+    scale = 1.0 / n if n % 128 else 1.0
+    d_s = spectra(T, n, h, scale)
+    got = d_s.cpu().numpy().view(np.complex64).reshape(channels, n)
+    ref = np.fft.fft(h.astype(np.float64), axis=-1) * scale
+    err = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    print(f"{T} N={n} spectra: rel_l2={err:.3e}", flush=True)
+    assert np.all(np.isfinite(got)) and err <= 2e-6
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+def test_async_equals_sync_and_scale(T):
+    n, batch, channels = 1024, 7, 6
+    rng = np.random.default_rng(17)
+    x = represent(rng.uniform(0, 1, size=(batch, channels, n)), T)
+    h = rng.uniform(0, 1.0 / n, size=(channels, n)).astype(np.float32)
+    raw, _ = convolve(T, n, x, spectra(T, n, h, 1.0), channels)
+    raw_async, _ = convolve(T, n, x, spectra(T, n, h, 1.0), channels, sync=False)
+    assert np.array_equal(raw, raw_async)
+    normed, _ = convolve(T, n, x, spectra(T, n, h, 1.0 / n), channels)
+    # scale = 1 writes N * (x (*) h), scale = 1/N writes x (*) h
+    err, _ = rel_l2(raw / n, normed)
+    assert err <= TIGHT[T], err
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("n,batch,channels", [(1024, 255, 257), (4096, 33, 64)])
+def test_full_size_impulse_rolls(T, n, batch, channels):
+    """Filter d is a unit impulse at tap s_d = (17 d + 1) mod N, so every output
+    row is its input row rolled by s_d (checked over all signals)."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    shifts = (17 * np.arange(channels) + 1) % n
+    h = np.zeros((channels, n), dtype=np.float32)
+    h[np.arange(channels), shifts] = 1.0
+    count = batch * channels * n
+    thff.ThunderFFTInitialize(T, n)
+    d_x = torch.empty(count, dtype=torch.float32 if T == "float" else torch.float16, device="cuda")
+    d_x.uniform_(-1, 1)
+    x = from_device(d_x, T).reshape(batch, channels, n)
+    d_spec = spectra(T, n, h, 1.0 / n)
+    d_y = torch.full_like(d_x, float("nan"))
+    thff.ThunderFFT_conv1d_real(T, n, d_x, d_spec, d_y, batch, channels)
+    y = from_device(d_y, T).reshape(batch, channels, n)
+    idx = (np.arange(n)[None, :] - shifts[:, None]) % n  # y[k] = x[(k - s) mod N]
+    expect = np.take_along_axis(x, np.broadcast_to(idx, x.shape), axis=-1)
+    err = np.abs(y - expect)
+    tol = (1e-5 if T == "float" else 2.0 ** -11) * np.abs(expect) + 2e-6
+    label = f"{T} N={n} B={batch} D={channels}: max_err={err.max():.3e}"
+    print(label, flush=True)
+    assert np.all(np.isfinite(y)) and np.all(err <= tol), label

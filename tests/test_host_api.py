@@ -99,3 +99,34 @@ def test_conv2d_argument_checks():
     for args in ((0, 16, 24), (8, 0, 24), (8, 16, 0), (8, 16, 8), (8, 16, 16)):
         with pytest.raises(ValueError):
             thff.ThunderFFT_conv2d("float", 64, 64, *args, 1)
+
+
+def test_conv1d_real_argument_checks():
+    """thff_conv1d_real and its filter preparation reject bad arguments before
+    any HIP call; the signal and output must be 16-byte aligned."""
+    conv, filt = thff.ThunderFFT_conv1d_real, thff.ThunderFFT_conv1d_real_filter
+    with pytest.raises(ValueError, match="nonnegative"):
+        conv("half", 256, 16, 32, 48, -1, 1)
+    conv("half", 256, 0, 0, 0, 0, 1)  # zero batch: no-op
+    with pytest.raises(ValueError, match="channels must be positive"):
+        conv("half", 256, 16, 32, 48, 1, 0)
+    for args in ((0, 32, 48), (16, 0, 48), (16, 32, 0), (16, 32, 16), (16, 32, 32)):
+        with pytest.raises(ValueError):
+            conv("half", 256, *args, 1, 1)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        conv("half", 256, 24, 32, 48, 1, 1)
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        conv("float", 256, 16, 32, 56, 1, 1)
+    with pytest.raises(ValueError, match="Unsupported"):
+        conv("half", 200, 16, 32, 48, 1, 1)
+    with pytest.raises(ValueError):
+        conv("double", 256, 16, 32, 48, 1, 1)
+    # filter spectra
+    with pytest.raises(ValueError, match="nonnegative"):
+        filt("half", 256, 16, 32, -1)
+    filt("half", 256, 0, 0, 0)  # zero channels: no-op
+    for args in ((0, 32), (16, 0), (16, 16)):
+        with pytest.raises(ValueError):
+            filt("half", 256, *args, 1)
+    with pytest.raises(ValueError, match="Unsupported"):
+        filt("float", 8192, 16, 32, 1)

@@ -208,6 +208,53 @@ def test_circconv_matches_fft_product():
     assert rel(oracle.circconv2d(x2, h2), expect2) < 1e-13
 
 
+def test_circconv_channels_pinned():
+    """Real per-channel convolution: numpy's FFT product, a shifted impulse
+    (y = c * roll(x, k0): a correlation or a wrong channel would fail), the
+    tap truncation, and the complex per-signal oracle with expanded filters."""
+    rng = np.random.default_rng(5)
+    batch, channels, n = 2, 3, 32
+    x = rng.standard_normal((batch, channels, n))
+    h = rng.standard_normal((channels, n))
+    expect = np.fft.ifft(np.fft.fft(x) * np.fft.fft(h)[None]).real
+    y = oracle.circconv1d_channels(x, h)
+    assert rel(y, expect) < 1e-13
+    per_signal = oracle.circconv1d(x.reshape(-1, n), np.tile(h, (batch, 1)), True)
+    assert rel(y.reshape(-1, n), per_signal.real) < 1e-13
+    # impulse taps: channel d delays by d + 1 and scales by d + 2
+    imp = np.zeros((channels, n))
+    for d in range(channels):
+        imp[d, d + 1] = d + 2
+    yi = oracle.circconv1d_channels(x, imp)
+    for d in range(channels):
+        assert np.array_equal(yi[:, d], (d + 2) * np.roll(x[:, d], d + 1, axis=-1))
+    # only the first `taps` taps count
+    taps = 5
+    cut = h.copy()
+    cut[:, taps:] = 0
+    assert rel(oracle.circconv1d_channels(x, h, taps), oracle.circconv1d_channels(x, cut)) < 1e-15
+
+
+def test_conv_real_inputs_are_the_c_library_sequence():
+    """The sample's inputs: srand(42) then rand()/RAND_MAX per signal value and
+    (rand()/RAND_MAX)/n per tap, drawn through this process's C library (a
+    separate route into the same generator) and glibc's known first values."""
+    import ctypes
+
+    libc = ctypes.CDLL("libc.so.6")
+    rand_max = np.float32(2147483647)
+    n, taps, batch, channels = 64, 7, 3, 2
+    x, h = oracle.conv_real_inputs(n, taps, batch, channels, seed=42)
+    libc.srand(42)
+    draws = np.array([libc.rand() for _ in range(batch * channels * n + channels * taps)])
+    assert draws[0] == 71876166 and draws[1] == 708592740  # glibc, seed 42
+    ex = draws[: x.size].astype(np.float32) / rand_max
+    assert np.array_equal(x.reshape(-1), ex)
+    eh = np.zeros((channels, n), dtype=np.float32)
+    eh[:, :taps] = (draws[x.size:].astype(np.float32) / rand_max).reshape(channels, taps) / np.float32(n)
+    assert np.array_equal(h, eh)
+
+
 # ---------------------------------------------------------------- the gate has teeth
 def test_metrics_definition():
     ref = np.array([3 + 4j, 0, 1], dtype=np.complex128)

@@ -60,6 +60,12 @@ def lib() -> ctypes.CDLL:
         c2sig = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, vp, ctypes.c_int, vp]
         L.thff_conv2d.argtypes = c2sig
         L.thff_conv2d_async.argtypes = c2sig
+        rfsig = [ctypes.c_int, ctypes.c_int, vp, vp, ctypes.c_int, ctypes.c_float, vp]
+        L.thff_conv1d_real_filter.argtypes = rfsig
+        L.thff_conv1d_real_filter_async.argtypes = rfsig
+        rsig = [ctypes.c_int, ctypes.c_int, vp, vp, vp, ctypes.c_int, ctypes.c_int, vp]
+        L.thff_conv1d_real.argtypes = rsig
+        L.thff_conv1d_real_async.argtypes = rsig
         L.thff_twiddle_info.argtypes = [ctypes.c_int, ctypes.POINTER(vp),
                                         ctypes.POINTER(ctypes.c_int)]
         L.thff_fill_uniform.argtypes = [ctypes.c_int, vp, ctypes.c_longlong, ctypes.c_ulonglong,
@@ -144,6 +150,36 @@ def ThunderFFT_conv1d_async(T, N: int, d_x, d_h, d_y, batch: int, per_signal_fil
     """As ThunderFFT_conv1d, but returns once the launch is enqueued on ``stream``."""
     _raise(lib().thff_conv1d_async(_precision(T), int(N), _ptr(d_x), _ptr(d_h), _ptr(d_y),
                                    int(batch), int(bool(per_signal_filter)), _stream(stream)))
+
+
+def ThunderFFT_conv1d_real_filter(T, N: int, d_h, d_spectrum, channels: int, scale: float = 1.0,
+                                  stream=0) -> None:
+    """spectrum[d] = scale * FFT(h[d]) for real fp32 filters h (channels, N) -> complex64
+    spectra (channels, N), for ThunderFFT_conv1d_real of type T; synchronous."""
+    _raise(lib().thff_conv1d_real_filter(_precision(T), int(N), _ptr(d_h), _ptr(d_spectrum),
+                                         int(channels), float(scale), _stream(stream)))
+
+
+def ThunderFFT_conv1d_real_filter_async(T, N: int, d_h, d_spectrum, channels: int,
+                                        scale: float = 1.0, stream=0) -> None:
+    """As ThunderFFT_conv1d_real_filter, but returns once the launch is enqueued."""
+    _raise(lib().thff_conv1d_real_filter_async(_precision(T), int(N), _ptr(d_h), _ptr(d_spectrum),
+                                               int(channels), float(scale), _stream(stream)))
+
+
+def ThunderFFT_conv1d_real(T, N: int, d_x, d_spectrum, d_y, batch: int, channels: int,
+                           stream=0) -> None:
+    """Real fused convolution y[b][d] = Re IFFT(FFT(x[b][d]) * spectrum[d]) of real
+    (batch, channels, N) signals of type T; synchronous."""
+    _raise(lib().thff_conv1d_real(_precision(T), int(N), _ptr(d_x), _ptr(d_spectrum), _ptr(d_y),
+                                  int(batch), int(channels), _stream(stream)))
+
+
+def ThunderFFT_conv1d_real_async(T, N: int, d_x, d_spectrum, d_y, batch: int, channels: int,
+                                 stream=0) -> None:
+    """As ThunderFFT_conv1d_real, but returns once the launch is enqueued on ``stream``."""
+    _raise(lib().thff_conv1d_real_async(_precision(T), int(N), _ptr(d_x), _ptr(d_spectrum),
+                                        _ptr(d_y), int(batch), int(channels), _stream(stream)))
 
 
 def ThunderFFT_conv2d(T, rows: int, cols: int, d_x, d_h, d_y, batch: int, stream=0) -> None:

@@ -112,6 +112,35 @@ hipError_t launch_conv1d(int precision, bool per_signal_filter, const void* x, c
     return hipGetLastError();
 }
 
+template <int N>
+hipError_t launch_conv1d_real_filter(const float* h, float2* spectrum, int channels, float scale,
+                                     const float2* tw, hipStream_t stream) {
+    const unsigned grid =
+        static_cast<unsigned>((channels + C2CPlan<N>::kFPB - 1) / C2CPlan<N>::kFPB);
+    conv1d_real_filter_kernel<N><<<grid, 256, 0, stream>>>(h, spectrum, channels, scale, tw);
+    return hipGetLastError();
+}
+
+template <int N>
+hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectrum, void* y,
+                              int batch, int channels, const float2* tw, int num_cus,
+                              hipStream_t stream) {
+    using P = C2CPlan<N>;
+    const long long transforms = (static_cast<long long>(batch) + 1) / 2 * channels;
+    const long long ntiles = (transforms + P::kFPB - 1) / P::kFPB;
+    const int tpb = ntiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? 2 : 1;
+    const unsigned grid = static_cast<unsigned>((ntiles + tpb - 1) / tpb);
+    if (precision == 0)
+        conv1d_real_kernel<float2, N><<<grid, 256, 0, stream>>>(
+            static_cast<const float*>(x), spectrum, static_cast<float*>(y), batch, channels, tw,
+            tpb);
+    else
+        conv1d_real_kernel<__half2, N><<<grid, 256, 0, stream>>>(
+            static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch, channels, tw,
+            tpb);
+    return hipGetLastError();
+}
+
 #if THFF_N == 64
 hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y, int batch,
                            const float2* tw, int num_cus, hipStream_t stream) {
@@ -136,5 +165,9 @@ template hipError_t launch_c2c<THFF_N>(int, bool, const void*, void*, int, const
                                        hipStream_t);
 template hipError_t launch_conv1d<THFF_N>(int, bool, const void*, const void*, void*, int,
                                           const float2*, int, hipStream_t);
+template hipError_t launch_conv1d_real_filter<THFF_N>(const float*, float2*, int, float,
+                                                      const float2*, hipStream_t);
+template hipError_t launch_conv1d_real<THFF_N>(int, const void*, const float2*, void*, int, int,
+                                               const float2*, int, hipStream_t);
 
 }  // namespace thff

@@ -94,6 +94,39 @@ hipError_t dispatch_conv1d(int n, int precision, bool per_signal, const void* x,
     }
 }
 
+hipError_t dispatch_conv1d_real_filter(int n, const float* h, float2* spectrum, int channels,
+                                       float scale, const float2* tw, hipStream_t s) {
+    switch (n) {
+    case 64: return thff::launch_conv1d_real_filter<64>(h, spectrum, channels, scale, tw, s);
+    case 128: return thff::launch_conv1d_real_filter<128>(h, spectrum, channels, scale, tw, s);
+    case 256: return thff::launch_conv1d_real_filter<256>(h, spectrum, channels, scale, tw, s);
+    case 512: return thff::launch_conv1d_real_filter<512>(h, spectrum, channels, scale, tw, s);
+    case 1024: return thff::launch_conv1d_real_filter<1024>(h, spectrum, channels, scale, tw, s);
+    case 2048: return thff::launch_conv1d_real_filter<2048>(h, spectrum, channels, scale, tw, s);
+    case 4096: return thff::launch_conv1d_real_filter<4096>(h, spectrum, channels, scale, tw, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t dispatch_conv1d_real(int n, int precision, const void* x, const float2* spectrum,
+                                void* y, int batch, int channels, const float2* tw, int cus,
+                                hipStream_t s) {
+#define THFF_REAL_CASE(L)                                                                     \
+    case L:                                                                                   \
+        return thff::launch_conv1d_real<L>(precision, x, spectrum, y, batch, channels, tw, cus, s)
+    switch (n) {
+        THFF_REAL_CASE(64);
+        THFF_REAL_CASE(128);
+        THFF_REAL_CASE(256);
+        THFF_REAL_CASE(512);
+        THFF_REAL_CASE(1024);
+        THFF_REAL_CASE(2048);
+        THFF_REAL_CASE(4096);
+    default: return hipErrorInvalidValue;
+    }
+#undef THFF_REAL_CASE
+}
+
 // The current device's cached table for (precision, n) and its CU count, or
 // an error message naming the missing ThunderFFTInitialize call.
 int cached_table(int precision, int n, const char* who, const float2** table, int* cus) {
@@ -142,6 +175,64 @@ int conv1d_impl(int precision, int n, const void* x, const void* h, void* y, int
         if (err != hipSuccess) return fail_hip(err, "ThunderFFT_conv1d synchronize");
     }
     return THFF_OK;
+}
+
+int finish(hipStream_t s, bool synchronize, const char* who) {
+    if (!synchronize) return THFF_OK;
+    const hipError_t err = hipStreamSynchronize(s);
+    return err == hipSuccess ? THFF_OK : fail_hip(err, who);
+}
+
+int conv1d_real_filter_impl(int precision, int n, const void* h, void* spectrum, int channels,
+                            float scale, void* stream, bool synchronize) {
+    if (!supported_precision(precision))
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d_real_filter supports float and half only");
+    if (!supported_length(n)) return fail(THFF_EINVAL, "Unsupported ThunderFFT length");
+    if (channels < 0) return fail(THFF_EINVAL, "ThunderFFT channels must be nonnegative");
+    if (channels == 0) return THFF_OK;
+    if (!h || !spectrum)
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d_real_filter requires non-null filter and spectrum");
+    if (spectrum == h)
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d_real_filter spectrum must not alias the filter");
+    const float2* table = nullptr;
+    int cus = 0;
+    const int rc = cached_table(precision, n, "ThunderFFT_conv1d_real_filter", &table, &cus);
+    if (rc != THFF_OK) return rc;
+    auto s = static_cast<hipStream_t>(stream);
+    const hipError_t err = dispatch_conv1d_real_filter(
+        n, static_cast<const float*>(h), static_cast<float2*>(spectrum), channels, scale, table, s);
+    if (err != hipSuccess) return fail_hip(err, "ThunderFFT_conv1d_real_filter launch");
+    return finish(s, synchronize, "ThunderFFT_conv1d_real_filter synchronize");
+}
+
+int conv1d_real_impl(int precision, int n, const void* x, const void* spectrum, void* y,
+                     int batch, int channels, void* stream, bool synchronize) {
+    if (!supported_precision(precision))
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d_real supports float and half only");
+    if (!supported_length(n)) return fail(THFF_EINVAL, "Unsupported ThunderFFT length");
+    if (batch < 0) return fail(THFF_EINVAL, "ThunderFFT batch must be nonnegative");
+    if (batch == 0) return THFF_OK;
+    if (channels <= 0) return fail(THFF_EINVAL, "ThunderFFT channels must be positive");
+    if (!x || !spectrum || !y)
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d_real requires non-null signal, spectrum and output");
+    if (y == x || y == spectrum)
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d_real output must not alias its inputs");
+    if ((reinterpret_cast<std::uintptr_t>(x) | reinterpret_cast<std::uintptr_t>(y)) & 15)
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d_real requires 16-byte aligned signal and output");
+    // Complex transforms: one per pair of signals of a channel.
+    const long long transforms = (static_cast<long long>(batch) + 1) / 2 * channels;
+    const long long fpb = thff::c2c_transforms_per_block(n);
+    if ((transforms + fpb - 1) / fpb * 256 > static_cast<long long>(UINT32_MAX))
+        return fail(THFF_EINVAL, "ThunderFFT batch exceeds one launch for this length");
+    const float2* table = nullptr;
+    int cus = 0;
+    const int rc = cached_table(precision, n, "ThunderFFT_conv1d_real", &table, &cus);
+    if (rc != THFF_OK) return rc;
+    auto s = static_cast<hipStream_t>(stream);
+    const hipError_t err = dispatch_conv1d_real(n, precision, x, static_cast<const float2*>(spectrum),
+                                                y, batch, channels, table, cus, s);
+    if (err != hipSuccess) return fail_hip(err, "ThunderFFT_conv1d_real launch");
+    return finish(s, synchronize, "ThunderFFT_conv1d_real synchronize");
 }
 
 int conv2d_impl(int precision, int rows, int cols, const void* x, const void* h, void* y,
@@ -297,6 +388,26 @@ int thff_conv1d(int precision, int n, const void* d_x, const void* d_h, void* d_
 int thff_conv1d_async(int precision, int n, const void* d_x, const void* d_h, void* d_y,
                       int batch, int per_signal_filter, void* stream) {
     return conv1d_impl(precision, n, d_x, d_h, d_y, batch, per_signal_filter, stream, false);
+}
+
+int thff_conv1d_real_filter(int precision, int n, const void* d_h, void* d_spectrum,
+                            int channels, float scale, void* stream) {
+    return conv1d_real_filter_impl(precision, n, d_h, d_spectrum, channels, scale, stream, true);
+}
+
+int thff_conv1d_real_filter_async(int precision, int n, const void* d_h, void* d_spectrum,
+                                  int channels, float scale, void* stream) {
+    return conv1d_real_filter_impl(precision, n, d_h, d_spectrum, channels, scale, stream, false);
+}
+
+int thff_conv1d_real(int precision, int n, const void* d_x, const void* d_spectrum, void* d_y,
+                     int batch, int channels, void* stream) {
+    return conv1d_real_impl(precision, n, d_x, d_spectrum, d_y, batch, channels, stream, true);
+}
+
+int thff_conv1d_real_async(int precision, int n, const void* d_x, const void* d_spectrum,
+                           void* d_y, int batch, int channels, void* stream) {
+    return conv1d_real_impl(precision, n, d_x, d_spectrum, d_y, batch, channels, stream, false);
 }
 
 int thff_conv2d(int precision, int rows, int cols, const void* d_x, const void* d_h, void* d_y,

@@ -19,6 +19,19 @@ template <int N>
 hipError_t launch_conv1d(int precision, bool per_signal_filter, const void* x, const void* h,
                          void* y, int batch, const float2* tw, int num_cus, hipStream_t stream);
 
+// Enqueue the spectra of `channels` real fp32 filters h[d] (N taps each):
+// spectrum[d][k] = scale * FFT(h[d])[k], fp32 complex.
+template <int N>
+hipError_t launch_conv1d_real_filter(const float* h, float2* spectrum, int channels, float scale,
+                                     const float2* tw, hipStream_t stream);
+
+// Enqueue the fused real convolution of x[batch][channels][N] (float or half)
+// with the channel spectra: y[b][d] = IFFT(FFT(x[b][d]) * spectrum[d]), real.
+template <int N>
+hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectrum, void* y,
+                              int batch, int channels, const float2* tw, int num_cus,
+                              hipStream_t stream);
+
 // Enqueue the fused 2-D circular convolution of `batch` 64 x 64 images with
 // one shared 64 x 64 filter h (tw: the N = 64 table).
 hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y, int batch,
