@@ -148,6 +148,58 @@ def time_conv(kind: str, T: str, steps: int, warmup: int) -> dict:
             "bytes_per_call": nbytes}
 
 
+def time_conv_real(T: str, n: int, steps: int, warmup: int) -> dict:
+    """The reference's real-input fused convolution
+    (sample/conv1d/conv1d_fullfft_l4096_thunder.cu:280-331) at 2^26 real samples:
+    16384 signals [B=16384*4096/(n*64)][D=64][n], one real 9-tap filter per
+    channel (the sample's default K) whose spectra are prepared once outside
+    the timed region (its include_filter_fft=0 mode)."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    channels = 64
+    count = 1 << 26
+    batch = count // (n * channels)
+    dt = torch.float32 if T == "float" else torch.float16
+    elem = 4 if T == "float" else 2
+    gen = torch.Generator(device="cuda").manual_seed(n)
+    x = torch.rand(count, device="cuda", generator=gen).to(dt)
+    y = torch.empty_like(x)
+    h = torch.zeros(channels, n, device="cuda")
+    h[:, :9] = torch.rand(channels, 9, device="cuda", generator=gen) / n
+    spectrum = torch.empty(channels * n * 2, device="cuda")
+    stream = torch.cuda.current_stream()
+    thff.ThunderFFTInitialize(T, n)
+    thff.ThunderFFT_conv1d_real_filter(T, n, h, spectrum, channels, 1.0, stream)
+
+    def launch():
+        thff.ThunderFFT_conv1d_real_async(T, n, x, spectrum, y, batch, channels, stream)
+
+    for _ in range(warmup):
+        launch()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        launch()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    thff.ThunderFFTFinalize(T)
+    nbytes = 2 * count * elem  # x and y; the spectra (2 MiB) stay in L2
+    transforms = count // (2 * n)  # two real signals per complex transform
+    flops = transforms * (2 * 5.0 * n * math.log2(n) + 6.0 * n)
+    del x, y, h, spectrum
+    return {"workload": (f"conv1d_real [{batch}][{channels}][{n}] {T}, 9-tap real filters, "
+                         f"fused FFT * H * IFFT (two signals per complex transform)"),
+            "precision": T, "us_per_call": ms * 1e3, "gflops": flops / (ms * 1e-3) / 1e9,
+            "gbps": nbytes / (ms * 1e-3) / 1e9,
+            "pct_hbm_peak": 100.0 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+            "bytes_per_call": nbytes}
+
+
 def compute_differential(T: str, repeats: int = 1000, trials: int = 3) -> dict:
     """Reference-style compute time of the N=1024, batch-65536 transform
     (sample/bench/paper_fft.cu:131-148): one launch loads every tile once,
@@ -298,6 +350,12 @@ def main():
         print(f"[bench] {r['workload']}: {r['us_per_call']:.1f} us, {r['gbps']:.0f} GB/s "
               f"({r['pct_hbm_peak']:.1f}% of HBM peak), {r['gflops']:.0f} GFLOP/s",
               file=sys.stderr, flush=True)
+    for T, n in (("half", 4096), ("half", 1024), ("half", 256), ("float", 4096)):
+        r = time_conv_real(T, n, max(1, a.steps // 2), max(1, a.warmup // 2))
+        runs[f"conv1d_real_{T}_n{n}"] = r
+        print(f"[bench] {r['workload']}: {r['us_per_call']:.1f} us, {r['gbps']:.0f} GB/s "
+              f"({r['pct_hbm_peak']:.1f}% of HBM peak), {r['gflops']:.0f} GFLOP/s",
+              file=sys.stderr, flush=True)
     for T in ("float", "half"):
         r = compute_differential(T)
         runs[f"compute_{T}"] = r
@@ -340,7 +398,8 @@ def main():
         out["also"][k]["hbm_traffic_bytes"] = load_traffic(k)
     out["also"]["conv_note"] = ("conv1d bytes = x, h and y (3 * 2^25 complex); conv2d bytes = x "
                                 "and y (2 * 2^25 complex; the 32 KiB filter is read per "
-                                "workgroup from L2); GFLOP/s counts 5 N log2 N per transform")
+                                "workgroup from L2); conv1d_real bytes = x and y (2 * 2^26 "
+                                "real samples); GFLOP/s counts 5 N log2 N per transform")
     print(json.dumps(out), flush=True)
 
 
