@@ -334,3 +334,108 @@ __global__ __launch_bounds__(256) void conv1d_real_kernel(
 }
 
 }  // namespace thff
+
+namespace thff {
+
+// ---------------------------------------------------------------------------
+// Tiled valid 1-D correlation with 64-point FFTs (overlap-save), the
+// reference's conv1d_direct_fft_kernel (sample/conv1d/main.cu:38-128):
+//   y[b][i] = sum_{k < F} x[b][i + k] * f[k],   i < L - F + 1,  1 <= F <= 64,
+// complex x, f, no conjugation.  Window w of a signal is x[w*V .. w*V + 63]
+// with V = 65 - F; its circular convolution with g[m] = f[(64 - m) mod 64] / 64
+// (the reversed filter, main.cu:145-154) equals y[w*V + j] for j < V, since
+// those outputs never wrap.  Each wave owns 16 consecutive windows: it stages
+// their input span (15 V + 64 <= 1024 values) in its own LDS region, gathers
+// every window into its transform slot's registers, runs FFT * G * IFFT and
+// writes the V valid outputs of each window back contiguously.  Nothing
+// crosses waves, so the kernel has no workgroup barrier.  Every workgroup
+// transforms the filter once (fp32 taps) and keeps G in registers.
+// Inputs past the end of a signal read as zero; no valid output uses them.
+// ---------------------------------------------------------------------------
+template <class IO>
+__global__ __launch_bounds__(256) void conv1d_valid_kernel(
+    const IO* __restrict__ x, const float2* __restrict__ taps, IO* __restrict__ y,
+    long long len, int ntaps, int batch, const float2* __restrict__ tw, int groups_per_block) {
+    using P = C2CPlan<64>;
+    using I = Io<IO>;
+    constexpr int kWindowsPerWave = 16;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int t = tid & 3;                   // lane within its window's transform
+    const int fl = (tid >> 2) & 15;          // window within the wave
+    __shared__ cpx lds[P::kLdsSlots];
+    cpx* const region = lds + wave * kWindowsPerWave * P::kSlot;  // 16 slots: 1088 >= 15 V + 64
+    cpx* const slot = region + fl * P::kSlot;
+
+    LaneTwiddles<64> w;
+    w.load(t, tw);
+
+    const int V = 65 - ntaps;                            // valid outputs per window
+    const unsigned rcpV = (65536u + V - 1) / V;          // e / V == (e * rcpV) >> 16 for e < 1024
+    const long long out_len = len - ntaps + 1;
+    const long long windows = (out_len + V - 1) / V;     // per signal
+    const long long groups_per_signal = (windows + P::kFPB - 1) / P::kFPB;
+    const long long groups = groups_per_signal * batch;
+
+    // G = FFT(g), g[m] = f[(64 - m) mod 64] / 64, m = t + 4 j.
+    cpx G[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int m = t + 4 * j;
+        const int k = m == 0 ? 0 : 64 - m;
+        const float2 c = k < ntaps ? taps[k] : make_float2(0.f, 0.f);
+        G[j] = {c.x * (1.0f / 64), c.y * (1.0f / 64)};
+    }
+    fft_registers<64, true>(G, slot, t, w);
+
+    long long g = static_cast<long long>(blockIdx.x) * groups_per_block;
+    const long long g_end = g + groups_per_block < groups ? g + groups_per_block : groups;
+    for (; g < g_end; ++g) {
+        const long long b = g / groups_per_signal;
+        // First window of this wave, and where its span starts in signal b.
+        const long long w0 = (g - b * groups_per_signal) * P::kFPB + wave * kWindowsPerWave;
+        const long long span0 = w0 * V;
+        const int span = 15 * V + 64;
+        const long long avail = len - span0;  // may be <= 0 past the last window
+        const IO* src = x + b * len + span0;
+
+        wave_lds_sync();  // the previous group's reads of the region are done
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int e = lane + 64 * i;
+            if (e < span)
+                region[e] = e < avail ? I::decode1(*reinterpret_cast<const typename I::W1*>(src + e))
+                                      : cpx{0.f, 0.f};
+        }
+        wave_lds_sync();
+        cpx v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = region[fl * V + t + 4 * j];
+        wave_lds_sync();  // the gather is done before the transform reuses the region
+
+        fft_registers<64, true>(v, slot, t, w);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = cmul(v[j], G[j]);
+        fft_registers<64, false>(v, slot, t, w);
+
+        wave_lds_sync();
+#pragma unroll
+        for (int j = 0; j < 16; ++j) slot[lds_pad(t + 4 * j)] = v[j];
+        wave_lds_sync();
+        // Outputs [w0 V, (w0 + 16) V) of signal b: window e / V, element e mod V.
+        const long long o0 = span0;
+        IO* dst = y + b * out_len + o0;
+        const long long left = out_len - o0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int e = lane + 64 * i;
+            if (e < kWindowsPerWave * V && e < left) {
+                const int q = static_cast<int>((static_cast<unsigned>(e) * rcpV) >> 16);
+                const int j = e - q * V;
+                *reinterpret_cast<typename I::W1*>(dst + e) =
+                    I::encode1(region[q * P::kSlot + lds_pad(j)]);
+            }
+        }
+    }
+}
+
+}  // namespace thff

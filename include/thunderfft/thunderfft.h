@@ -134,6 +134,26 @@ int thff_conv1d_real(int precision, int n, const void* d_x, const void* d_spectr
 int thff_conv1d_real_async(int precision, int n, const void* d_x, const void* d_spectrum,
                            void* d_y, int batch, int channels, void* stream);
 
+/* Tiled valid 1-D correlation with 64-point FFT windows (overlap-save), the
+ * reference's conv1d_direct_fft_kernel (sample/conv1d/main.cu:38-128, driven
+ * by main :207-336 with the definition of :156-174):
+ *   y[b][i] = sum_{k < filter_len} x[b][i + k] * taps[k],  i < input_len - filter_len + 1,
+ * complex, no conjugation.  x holds batch signals of input_len values and y
+ * batch outputs of input_len - filter_len + 1 values, both in `precision`
+ * storage; taps are filter_len fp32 complex values (float2) for both
+ * precisions.  1 <= filter_len <= 64 and input_len >= filter_len (the
+ * sample's checks, main.cu:223-230), THFF_EINVAL otherwise; batch < 0, null,
+ * aliased or misaligned pointers are THFF_EINVAL, batch = 0 is a no-op.
+ * Requires thff_initialize(precision, 64) (the windows are 64-point
+ * transforms).  Synchronises `stream` before returning. */
+int thff_conv1d_valid(int precision, const void* d_x, long long input_len, const void* d_taps,
+                      int filter_len, void* d_y, int batch, void* stream);
+
+/* thff_conv1d_valid without the final stream synchronisation. */
+int thff_conv1d_valid_async(int precision, const void* d_x, long long input_len,
+                            const void* d_taps, int filter_len, void* d_y, int batch,
+                            void* stream);
+
 /* Fused 2-D circular convolution of `batch` rows x cols row-major images with
  * one shared rows x cols filter (no function counterpart in the reference
  * library; the reference's 2-D convolution is the sample

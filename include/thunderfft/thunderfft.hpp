@@ -135,6 +135,18 @@ inline void ThunderFFT_conv1d_real(const T* d_x, const float2* d_spectrum, T* d_
                                    channels, static_cast<void*>(stream)));
 }
 
+// Tiled valid 1-D correlation y[b][i] = sum_k x[b][i + k] * taps[k] of `batch`
+// signals of input_len values with 1 <= filter_len <= 64 fp32 complex taps,
+// through 64-point FFT windows (the reference's sample/conv1d/main.cu:38-174).
+// y holds batch * (input_len - filter_len + 1) values; Initialize<T>(64) first.
+template <typename T>
+inline void ThunderFFT_conv1d_valid(const vec2_t<T>* d_x, long long input_len,
+                                    const float2* d_taps, int filter_len, vec2_t<T>* d_y,
+                                    int batch = 1, hipStream_t stream = 0) {
+    detail::check(thff_conv1d_valid(detail::precision_code<T>(), d_x, input_len, d_taps,
+                                    filter_len, d_y, batch, static_cast<void*>(stream)));
+}
+
 // Fused 2-D circular convolution of `batch` Rows x Cols images with one shared
 // filter: y[b] = IFFT2(FFT2(x[b]) * FFT2(h)) / (Rows*Cols).  Rows = Cols = 64;
 // Initialize<T>(64) first.  No counterpart in the reference's library API

@@ -62,6 +62,10 @@ def lib():
                                                    ctypes.c_int, dp, dp, dp]
         L.thff_conv_real_inputs.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_long,
                                             ctypes.c_int, ctypes.c_uint, fp, fp]
+        L.thff_conv1d_valid_f64.argtypes = [ctypes.c_long, ctypes.c_int, ctypes.c_long, dp, dp,
+                                            dp]
+        L.thff_conv1d_valid_inputs.argtypes = [ctypes.c_long, ctypes.c_int, ctypes.c_uint, fp,
+                                               fp]
         _lib = L
     return _lib
 
@@ -226,3 +230,28 @@ def conv_real_inputs(n: int, taps: int, batch: int, channels: int, seed: int = 4
                                        _p(x, ctypes.c_float), _p(h, ctypes.c_float)),
            "conv_real_inputs")
     return x, h
+
+
+def conv1d_valid(x, f) -> np.ndarray:
+    """Valid complex correlation y[..., i] = sum_k x[..., i + k] * f[k] (fp64, no
+    conjugation), sample/conv1d/main.cu:156-174.  x: (..., L), f: (F,)."""
+    x = _as_c128(x)
+    f = _as_c128(f).reshape(-1)
+    length, ntaps = x.shape[-1], f.size
+    out = np.empty(x.shape[:-1] + (length - ntaps + 1,), dtype=np.complex128)
+    _check(lib().thff_conv1d_valid_f64(length, ntaps, x.size // length,
+                                       _p(x.view(np.float64), ctypes.c_double),
+                                       _p(f.view(np.float64), ctypes.c_double),
+                                       _p(out.view(np.float64), ctypes.c_double)), "conv1d_valid")
+    return out
+
+
+def conv1d_valid_inputs(length: int, ntaps: int, seed: int = 42):
+    """The tiled-conv sample's inputs after srand(seed): complex64 x (length,) then
+    taps (ntaps,), each component rand()/RAND_MAX.  sample/conv1d/main.cu:130-135,233,260-262."""
+    x = np.empty(length, dtype=np.complex64)
+    f = np.empty(ntaps, dtype=np.complex64)
+    _check(lib().thff_conv1d_valid_inputs(length, ntaps, seed, _p(x.view(np.float32), ctypes.c_float),
+                                          _p(f.view(np.float32), ctypes.c_float)),
+           "conv1d_valid_inputs")
+    return x, f

@@ -32,6 +32,8 @@
  *     thff_circconv1d_channels_f64
  *   - the real convolution sample's seeded inputs (srand/rand,
  *     conv1d_fullfft_l4096_thunder.cu:389-401) -> thff_conv_real_inputs
+ *   - the tiled valid correlation of sample/conv1d/main.cu:156-174 and that
+ *     sample's seeded inputs -> thff_conv1d_valid_f64, thff_conv1d_valid_inputs
  *
  * Pinning: every function here is checked in tests/test_oracle.py against
  * closed forms (impulse/constant/tone spectra), invariants (Parseval,
@@ -529,5 +531,43 @@ int thff_conv_real_inputs(int n, int taps, long signals, int channels, unsigned 
     for (int d = 0; d < channels; ++d)
         for (int k = 0; k < taps; ++k)
             h[(size_t)d * n + k] = ((float)rand() / (float)RAND_MAX) / (float)n;
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Valid complex correlation, the tiled-conv sample's definition            */
+/* (sample/conv1d/main.cu:156-174, no conjugation), per signal b:           */
+/*   y[b][i] = sum_{k < ntaps} x[b][i + k] * f[k],  i < len - ntaps + 1.    */
+/* Interleaved complex doubles.                                             */
+/* ------------------------------------------------------------------------ */
+int thff_conv1d_valid_f64(long len, int ntaps, long batch, const double* x, const double* f,
+                          double* y) {
+    if (ntaps < 1 || len < ntaps || batch < 0) return -1;
+    const long out = len - ntaps + 1;
+    for (long b = 0; b < batch; ++b) {
+        const double* xs = x + 2 * (size_t)b * len;
+        double* ys = y + 2 * (size_t)b * out;
+        for (long i = 0; i < out; ++i) {
+            double sr = 0, si = 0;
+            for (int k = 0; k < ntaps; ++k) {
+                const double ar = xs[2 * (i + k)], ai = xs[2 * (i + k) + 1];
+                sr += ar * f[2 * k] - ai * f[2 * k + 1];
+                si += ar * f[2 * k + 1] + ai * f[2 * k];
+            }
+            ys[2 * i] = sr;
+            ys[2 * i + 1] = si;
+        }
+    }
+    return 0;
+}
+
+/* The tiled-conv sample's inputs (sample/conv1d/main.cu:233,130-135,260-262): */
+/* after srand(seed), len complex inputs then ntaps complex taps, each value  */
+/* (rand()/RAND_MAX, rand()/RAND_MAX) as fp32 (real drawn first).             */
+int thff_conv1d_valid_inputs(long len, int ntaps, unsigned seed, float* x, float* f) {
+    if (len < 0 || ntaps < 0) return -1;
+    srand(seed);
+    for (size_t i = 0; i < 2 * (size_t)len; ++i) x[i] = (float)rand() / (float)RAND_MAX;
+    for (int i = 0; i < 2 * ntaps; ++i) f[i] = (float)rand() / (float)RAND_MAX;
     return 0;
 }

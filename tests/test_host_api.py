@@ -130,3 +130,28 @@ def test_conv1d_real_argument_checks():
             filt("half", 256, *args, 1)
     with pytest.raises(ValueError, match="Unsupported"):
         filt("float", 8192, 16, 32, 1)
+
+
+def test_conv1d_valid_argument_checks():
+    """thff_conv1d_valid: the sample's two checks (1 <= filter_len <= 64,
+    input_len >= filter_len), then batch, pointers, aliasing and alignment,
+    all before any HIP call."""
+    v = thff.ThunderFFT_conv1d_valid
+    for ntaps in (0, 65, -1):
+        with pytest.raises(ValueError, match="filter_len"):
+            v("half", 16, 100, 32, ntaps, 48, 1)
+    with pytest.raises(ValueError, match="input_len"):
+        v("half", 16, 8, 32, 9, 48, 1)
+    with pytest.raises(ValueError, match="nonnegative"):
+        v("half", 16, 100, 32, 9, 48, -1)
+    v("half", 0, 100, 0, 9, 0, 0)  # zero batch: no-op
+    for args in ((0, 32, 48), (16, 0, 48), (16, 32, 0), (16, 32, 16), (16, 32, 32)):
+        x, f, y = args
+        with pytest.raises(ValueError):
+            v("half", x, 100, f, 9, y, 1)
+    with pytest.raises(ValueError, match="misaligned"):
+        v("float", 20, 100, 32, 9, 48, 1)   # float2 input not 8-byte aligned
+    with pytest.raises(ValueError, match="misaligned"):
+        v("half", 16, 100, 36, 9, 48, 1)    # fp32 complex taps not 8-byte aligned
+    with pytest.raises(ValueError):
+        v("double", 16, 100, 32, 9, 48, 1)

@@ -290,3 +290,34 @@ def test_gate_rejects_planted_mistakes(n):
     # inverse with a 1/N normalization the reference does not apply
     scaled = oracle.fft(ref, False) / n
     assert oracle.metrics(scaled.astype(np.complex64), n * x)["rel_l2"] > 100 * GATE
+
+
+def test_conv1d_valid_pinned():
+    """Valid correlation: numpy.convolve with the reversed filter (a library
+    routine), a shifted impulse (y[i] = c * x[i + k0]; conjugating the taps or
+    flipping the direction fails it), F = 1 and F = L, and batched rows."""
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((3, 50)) + 1j * rng.standard_normal((3, 50))
+    f = rng.standard_normal(9) + 1j * rng.standard_normal(9)
+    y = oracle.conv1d_valid(x, f)
+    assert y.shape == (3, 42)
+    for b in range(3):
+        assert rel(y[b], np.convolve(x[b], f[::-1], mode="valid")) < 1e-13
+    imp = np.zeros(9, dtype=complex)
+    imp[4] = 2 - 1j
+    assert np.array_equal(oracle.conv1d_valid(x, imp), (2 - 1j) * x[:, 4:46])
+    assert rel(oracle.conv1d_valid(x, f[:1]), x * f[0]) < 1e-15
+    assert rel(oracle.conv1d_valid(x[:, :9], f)[:, 0], x[:, :9] @ f) < 1e-13
+
+
+def test_conv1d_valid_inputs_are_the_c_library_sequence():
+    import ctypes
+
+    libc = ctypes.CDLL("libc.so.6")
+    rand_max = np.float32(2147483647)
+    length, ntaps = 40, 5
+    x, f = oracle.conv1d_valid_inputs(length, ntaps, seed=42)
+    libc.srand(42)
+    draws = np.array([libc.rand() for _ in range(2 * (length + ntaps))]).astype(np.float32) / rand_max
+    assert np.array_equal(x.view(np.float32), draws[: 2 * length])
+    assert np.array_equal(f.view(np.float32), draws[2 * length:])

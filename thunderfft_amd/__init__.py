@@ -66,6 +66,9 @@ def lib() -> ctypes.CDLL:
         rsig = [ctypes.c_int, ctypes.c_int, vp, vp, vp, ctypes.c_int, ctypes.c_int, vp]
         L.thff_conv1d_real.argtypes = rsig
         L.thff_conv1d_real_async.argtypes = rsig
+        vsig = [ctypes.c_int, vp, ctypes.c_longlong, vp, ctypes.c_int, vp, ctypes.c_int, vp]
+        L.thff_conv1d_valid.argtypes = vsig
+        L.thff_conv1d_valid_async.argtypes = vsig
         L.thff_twiddle_info.argtypes = [ctypes.c_int, ctypes.POINTER(vp),
                                         ctypes.POINTER(ctypes.c_int)]
         L.thff_fill_uniform.argtypes = [ctypes.c_int, vp, ctypes.c_longlong, ctypes.c_ulonglong,
@@ -180,6 +183,21 @@ def ThunderFFT_conv1d_real_async(T, N: int, d_x, d_spectrum, d_y, batch: int, ch
     """As ThunderFFT_conv1d_real, but returns once the launch is enqueued on ``stream``."""
     _raise(lib().thff_conv1d_real_async(_precision(T), int(N), _ptr(d_x), _ptr(d_spectrum),
                                         _ptr(d_y), int(batch), int(channels), _stream(stream)))
+
+
+def ThunderFFT_conv1d_valid(T, d_x, input_len: int, d_taps, filter_len: int, d_y, batch: int = 1,
+                            stream=0) -> None:
+    """Tiled valid correlation y[b][i] = sum_k x[b][i + k] * taps[k] (complex, type T;
+    taps complex64, 1 <= filter_len <= 64) through 64-point FFT windows; synchronous."""
+    _raise(lib().thff_conv1d_valid(_precision(T), _ptr(d_x), int(input_len), _ptr(d_taps),
+                                   int(filter_len), _ptr(d_y), int(batch), _stream(stream)))
+
+
+def ThunderFFT_conv1d_valid_async(T, d_x, input_len: int, d_taps, filter_len: int, d_y,
+                                  batch: int = 1, stream=0) -> None:
+    """As ThunderFFT_conv1d_valid, but returns once the launch is enqueued on ``stream``."""
+    _raise(lib().thff_conv1d_valid_async(_precision(T), _ptr(d_x), int(input_len), _ptr(d_taps),
+                                         int(filter_len), _ptr(d_y), int(batch), _stream(stream)))
 
 
 def ThunderFFT_conv2d(T, rows: int, cols: int, d_x, d_h, d_y, batch: int, stream=0) -> None:

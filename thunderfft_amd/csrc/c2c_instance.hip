@@ -142,6 +142,28 @@ hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectr
 }
 
 #if THFF_N == 64
+hipError_t launch_conv1d_valid(int precision, const void* x, long long len, const float2* taps,
+                               int ntaps, void* y, int batch, const float2* tw, int num_cus,
+                               hipStream_t stream) {
+    // A group is the 64 windows (one per transform slot) of one workgroup
+    // pass; a workgroup walks several when there are many, so its filter
+    // transform is shared.
+    const long long valid = 65 - ntaps;
+    const long long windows = (len - ntaps + 1 + valid - 1) / valid;
+    const long long groups = (windows + 63) / 64 * batch;
+    const int gpb = groups >= 16LL * (num_cus > 0 ? num_cus : 256) ? 4 : 1;
+    const unsigned grid = static_cast<unsigned>((groups + gpb - 1) / gpb);
+    if (precision == 0)
+        conv1d_valid_kernel<float2><<<grid, 256, 0, stream>>>(
+            static_cast<const float2*>(x), taps, static_cast<float2*>(y), len, ntaps, batch, tw,
+            gpb);
+    else
+        conv1d_valid_kernel<__half2><<<grid, 256, 0, stream>>>(
+            static_cast<const __half2*>(x), taps, static_cast<__half2*>(y), len, ntaps, batch, tw,
+            gpb);
+    return hipGetLastError();
+}
+
 hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y, int batch,
                            const float2* tw, int num_cus, hipStream_t stream) {
     // One image per tile; a workgroup transforms the filter once, so it

@@ -235,6 +235,41 @@ int conv1d_real_impl(int precision, int n, const void* x, const void* spectrum, 
     return finish(s, synchronize, "ThunderFFT_conv1d_real synchronize");
 }
 
+int conv1d_valid_impl(int precision, const void* x, long long input_len, const void* taps,
+                      int filter_len, void* y, int batch, void* stream, bool synchronize) {
+    if (!supported_precision(precision))
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d_valid supports float and half only");
+    // The reference sample's two argument checks (sample/conv1d/main.cu:223-230).
+    if (filter_len < 1 || filter_len > 64)
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d_valid: filter_len must be in [1, 64]");
+    if (input_len < filter_len)
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d_valid: input_len must be >= filter_len");
+    if (batch < 0) return fail(THFF_EINVAL, "ThunderFFT batch must be nonnegative");
+    if (batch == 0) return THFF_OK;
+    if (!x || !taps || !y)
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d_valid requires non-null input, filter and output");
+    if (y == x || y == taps)
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d_valid output must not alias its inputs");
+    const std::uintptr_t elem = precision == THFF_FLOAT ? 8 : 4;
+    if ((reinterpret_cast<std::uintptr_t>(x) | reinterpret_cast<std::uintptr_t>(y)) % elem ||
+        reinterpret_cast<std::uintptr_t>(taps) % 8)
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d_valid: misaligned pointer");
+    const long long valid = 65 - filter_len;
+    const long long windows = (input_len - filter_len + 1 + valid - 1) / valid;
+    if ((windows + 63) / 64 * batch * 256 > static_cast<long long>(UINT32_MAX))
+        return fail(THFF_EINVAL, "ThunderFFT batch exceeds one launch for this length");
+    const float2* table = nullptr;
+    int cus = 0;
+    const int rc = cached_table(precision, 64, "ThunderFFT_conv1d_valid", &table, &cus);
+    if (rc != THFF_OK) return rc;
+    auto s = static_cast<hipStream_t>(stream);
+    const hipError_t err = thff::launch_conv1d_valid(precision, x, input_len,
+                                                     static_cast<const float2*>(taps), filter_len,
+                                                     y, batch, table, cus, s);
+    if (err != hipSuccess) return fail_hip(err, "ThunderFFT_conv1d_valid launch");
+    return finish(s, synchronize, "ThunderFFT_conv1d_valid synchronize");
+}
+
 int conv2d_impl(int precision, int rows, int cols, const void* x, const void* h, void* y,
                 int batch, void* stream, bool synchronize) {
     if (!supported_precision(precision))
@@ -408,6 +443,19 @@ int thff_conv1d_real(int precision, int n, const void* d_x, const void* d_spectr
 int thff_conv1d_real_async(int precision, int n, const void* d_x, const void* d_spectrum,
                            void* d_y, int batch, int channels, void* stream) {
     return conv1d_real_impl(precision, n, d_x, d_spectrum, d_y, batch, channels, stream, false);
+}
+
+int thff_conv1d_valid(int precision, const void* d_x, long long input_len, const void* d_taps,
+                      int filter_len, void* d_y, int batch, void* stream) {
+    return conv1d_valid_impl(precision, d_x, input_len, d_taps, filter_len, d_y, batch, stream,
+                             true);
+}
+
+int thff_conv1d_valid_async(int precision, const void* d_x, long long input_len,
+                            const void* d_taps, int filter_len, void* d_y, int batch,
+                            void* stream) {
+    return conv1d_valid_impl(precision, d_x, input_len, d_taps, filter_len, d_y, batch, stream,
+                             false);
 }
 
 int thff_conv2d(int precision, int rows, int cols, const void* d_x, const void* d_h, void* d_y,

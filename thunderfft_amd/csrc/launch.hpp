@@ -32,6 +32,13 @@ hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectr
                               int batch, int channels, const float2* tw, int num_cus,
                               hipStream_t stream);
 
+// Enqueue the tiled valid correlation y[b][i] = sum_{k < ntaps} x[b][i + k] * taps[k]
+// (i < len - ntaps + 1, 1 <= ntaps <= 64) with 64-point FFT windows (tw: the
+// N = 64 table); taps are fp32 complex.
+hipError_t launch_conv1d_valid(int precision, const void* x, long long len, const float2* taps,
+                               int ntaps, void* y, int batch, const float2* tw, int num_cus,
+                               hipStream_t stream);
+
 // Enqueue the fused 2-D circular convolution of `batch` 64 x 64 images with
 // one shared 64 x 64 filter h (tw: the N = 64 table).
 hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y, int batch,
