@@ -200,6 +200,52 @@ def time_conv_real(T: str, n: int, steps: int, warmup: int) -> dict:
             "bytes_per_call": nbytes}
 
 
+def time_conv_valid(T: str, ntaps: int, steps: int, warmup: int) -> dict:
+    """The reference's tiled valid conv1d (sample/conv1d/main.cu:38-174) on one
+    complex signal of 2^26 samples with `ntaps` complex taps (its default is
+    9), 64-point FFT windows with 65 - ntaps valid outputs each."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    length = 1 << 26
+    out_len = length - ntaps + 1
+    dt = torch.float32 if T == "float" else torch.float16
+    elem = 8 if T == "float" else 4
+    gen = torch.Generator(device="cuda").manual_seed(ntaps)
+    x = torch.rand(2 * length, device="cuda", generator=gen).to(dt)
+    y = torch.empty(2 * out_len, dtype=dt, device="cuda")
+    taps = torch.rand(2 * ntaps, device="cuda", generator=gen)
+    stream = torch.cuda.current_stream()
+    thff.ThunderFFTInitialize(T, 64)
+
+    def launch():
+        thff.ThunderFFT_conv1d_valid_async(T, x, length, taps, ntaps, y, 1, stream)
+
+    for _ in range(warmup):
+        launch()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        launch()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    thff.ThunderFFTFinalize(T)
+    nbytes = (length + out_len) * elem
+    windows = -(-out_len // (65 - ntaps))
+    flops = windows * (2 * 5.0 * 64 * 6 + 6.0 * 64)
+    del x, y, taps
+    return {"workload": (f"conv1d_valid {length} x {ntaps} taps {T}2, 64-point windows "
+                         f"({65 - ntaps} outputs each)"),
+            "precision": T, "us_per_call": ms * 1e3, "gflops": flops / (ms * 1e-3) / 1e9,
+            "gbps": nbytes / (ms * 1e-3) / 1e9,
+            "pct_hbm_peak": 100.0 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
+            "bytes_per_call": nbytes}
+
+
 def compute_differential(T: str, repeats: int = 1000, trials: int = 3) -> dict:
     """Reference-style compute time of the N=1024, batch-65536 transform
     (sample/bench/paper_fft.cu:131-148): one launch loads every tile once,
@@ -356,6 +402,12 @@ def main():
         print(f"[bench] {r['workload']}: {r['us_per_call']:.1f} us, {r['gbps']:.0f} GB/s "
               f"({r['pct_hbm_peak']:.1f}% of HBM peak), {r['gflops']:.0f} GFLOP/s",
               file=sys.stderr, flush=True)
+    for T, ntaps in (("half", 9), ("float", 9)):
+        r = time_conv_valid(T, ntaps, max(1, a.steps // 2), max(1, a.warmup // 2))
+        runs[f"conv1d_valid_{T}_f{ntaps}"] = r
+        print(f"[bench] {r['workload']}: {r['us_per_call']:.1f} us, {r['gbps']:.0f} GB/s "
+              f"({r['pct_hbm_peak']:.1f}% of HBM peak), {r['gflops']:.0f} GFLOP/s",
+              file=sys.stderr, flush=True)
     for T in ("float", "half"):
         r = compute_differential(T)
         runs[f"compute_{T}"] = r
@@ -399,7 +451,8 @@ def main():
     out["also"]["conv_note"] = ("conv1d bytes = x, h and y (3 * 2^25 complex); conv2d bytes = x "
                                 "and y (2 * 2^25 complex; the 32 KiB filter is read per "
                                 "workgroup from L2); conv1d_real bytes = x and y (2 * 2^26 "
-                                "real samples); GFLOP/s counts 5 N log2 N per transform")
+                                "real samples); conv1d_valid bytes = x and y (2^26 + 2^26 - F + 1 "
+                                "complex); GFLOP/s counts 5 N log2 N per transform")
     print(json.dumps(out), flush=True)
 
 

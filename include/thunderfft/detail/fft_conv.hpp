@@ -348,22 +348,31 @@ namespace thff {
 // their input span (15 V + 64 <= 1024 values) in its own LDS region, gathers
 // every window into its transform slot's registers, runs FFT * G * IFFT and
 // writes the V valid outputs of each window back contiguously.  Nothing
-// crosses waves, so the kernel has no workgroup barrier.  Every workgroup
-// transforms the filter once (fp32 taps) and keeps G in registers.
+// crosses waves, so the kernel has no workgroup barrier after its set-up:
+// every workgroup transforms the filter once (fp32 taps) into a 64-value LDS
+// table G.
 // Inputs past the end of a signal read as zero; no valid output uses them.
+// Spans and output runs start at multiples of 16 values of their signal, so
+// signals that start on a 16-byte boundary move as whole 16-byte vectors
+// (one partial vector at a signal's end); others value by value.
 // ---------------------------------------------------------------------------
 template <class IO>
-__global__ __launch_bounds__(256) void conv1d_valid_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void conv1d_valid_kernel(
     const IO* __restrict__ x, const float2* __restrict__ taps, IO* __restrict__ y,
     long long len, int ntaps, int batch, const float2* __restrict__ tw, int groups_per_block) {
     using P = C2CPlan<64>;
     using I = Io<IO>;
+    using W1 = typename I::W1;
+    using W4 = typename I::W4;
+    constexpr int kVec = I::kVec;      // complex values per 16-byte vector
     constexpr int kWindowsPerWave = 16;
+    constexpr int kSpan = 1024;        // values staged per wave, >= 15 V + 64 and >= 16 V
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int t = tid & 3;                   // lane within its window's transform
-    const int fl = (tid >> 2) & 15;          // window within the wave
-    __shared__ cpx lds[P::kLdsSlots];
-    cpx* const region = lds + wave * kWindowsPerWave * P::kSlot;  // 16 slots: 1088 >= 15 V + 64
+    const int t = tid & 3;             // lane within its window's transform
+    const int fl = (tid >> 2) & 15;    // window within the wave
+    __shared__ __align__(16) cpx lds[P::kLdsSlots];
+    __shared__ cpx spectrum[64];  // G, natural order
+    cpx* const region = lds + wave * kWindowsPerWave * P::kSlot;  // 16 slots = 1088 >= kSpan
     cpx* const slot = region + fl * P::kSlot;
 
     LaneTwiddles<64> w;
@@ -375,36 +384,66 @@ __global__ __launch_bounds__(256) void conv1d_valid_kernel(
     const long long windows = (out_len + V - 1) / V;     // per signal
     const long long groups_per_signal = (windows + P::kFPB - 1) / P::kFPB;
     const long long groups = groups_per_signal * batch;
+    const bool x16 = (reinterpret_cast<unsigned long long>(x) & 15) == 0;
+    const bool y16 = (reinterpret_cast<unsigned long long>(y) & 15) == 0;
 
-    // G = FFT(g), g[m] = f[(64 - m) mod 64] / 64, m = t + 4 j.
-    cpx G[16];
+    // G = FFT(g), g[m] = f[(64 - m) mod 64] / 64, m = t + 4 j, computed by
+    // every slot and published once by the first slot.
+    {
+        cpx G[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int m = t + 4 * j;
-        const int k = m == 0 ? 0 : 64 - m;
-        const float2 c = k < ntaps ? taps[k] : make_float2(0.f, 0.f);
-        G[j] = {c.x * (1.0f / 64), c.y * (1.0f / 64)};
+        for (int j = 0; j < 16; ++j) {
+            const int m = t + 4 * j;
+            const int k = m == 0 ? 0 : 64 - m;
+            const float2 c = k < ntaps ? taps[k] : make_float2(0.f, 0.f);
+            G[j] = {c.x * (1.0f / 64), c.y * (1.0f / 64)};
+        }
+        fft_registers<64, true>(G, slot, t, w);
+        if (tid < 4)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) spectrum[t + 4 * j] = G[j];
+        __syncthreads();
     }
-    fft_registers<64, true>(G, slot, t, w);
 
     long long g = static_cast<long long>(blockIdx.x) * groups_per_block;
     const long long g_end = g + groups_per_block < groups ? g + groups_per_block : groups;
     for (; g < g_end; ++g) {
         const long long b = g / groups_per_signal;
-        // First window of this wave, and where its span starts in signal b.
+        // This wave's first window, and where its input span and its outputs
+        // start in signal b (both w0 * V, a multiple of 16 values).
         const long long w0 = (g - b * groups_per_signal) * P::kFPB + wave * kWindowsPerWave;
         const long long span0 = w0 * V;
-        const int span = 15 * V + 64;
-        const long long avail = len - span0;  // may be <= 0 past the last window
+        if (span0 >= out_len) continue;  // no window of this wave has an output
+        const long long avail = len - span0;  // > 0
         const IO* src = x + b * len + span0;
+        // Whole 16-byte vectors when the signal starts on one (always for b = 0).
+        const bool in_vec = x16 && (b * len) % kVec == 0;
+        const bool out_vec = y16 && (b * out_len) % kVec == 0;
 
         wave_lds_sync();  // the previous group's reads of the region are done
+        if (in_vec) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int e = lane + 64 * i;
-            if (e < span)
-                region[e] = e < avail ? I::decode1(*reinterpret_cast<const typename I::W1*>(src + e))
+            for (int i = 0; i < kSpan / (64 * kVec); ++i) {
+                const int e = kVec * (lane + 64 * i);
+                cpx q[kVec];
+                if (e + kVec <= avail) {
+                    I::decode4(*reinterpret_cast<const W4*>(src + e), q);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < kVec; ++c)
+                        q[c] = e + c < avail ? I::decode1(*reinterpret_cast<const W1*>(src + e + c))
+                                             : cpx{0.f, 0.f};
+                }
+#pragma unroll
+                for (int c = 0; c < kVec; ++c) region[e + c] = q[c];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kSpan / 64; ++i) {
+                const int e = lane + 64 * i;
+                region[e] = e < avail ? I::decode1(*reinterpret_cast<const W1*>(src + e))
                                       : cpx{0.f, 0.f};
+            }
         }
         wave_lds_sync();
         cpx v[16];
@@ -414,25 +453,42 @@ __global__ __launch_bounds__(256) void conv1d_valid_kernel(
 
         fft_registers<64, true>(v, slot, t, w);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = cmul(v[j], G[j]);
+        for (int j = 0; j < 16; ++j) v[j] = cmul(v[j], spectrum[t + 4 * j]);
         fft_registers<64, false>(v, slot, t, w);
 
         wave_lds_sync();
 #pragma unroll
         for (int j = 0; j < 16; ++j) slot[lds_pad(t + 4 * j)] = v[j];
         wave_lds_sync();
-        // Outputs [w0 V, (w0 + 16) V) of signal b: window e / V, element e mod V.
-        const long long o0 = span0;
-        IO* dst = y + b * out_len + o0;
-        const long long left = out_len - o0;
+        // Output e of the wave (e < 16 V) is element e mod V of window e / V.
+        const long long left = out_len - span0;
+        const int count = left < kWindowsPerWave * V ? static_cast<int>(left) : kWindowsPerWave * V;
+        IO* dst = y + b * out_len + span0;
+        auto value = [&](int e) {
+            const int q = static_cast<int>((static_cast<unsigned>(e) * rcpV) >> 16);
+            return region[q * P::kSlot + lds_pad(e - q * V)];
+        };
+        if (out_vec) {
+#pragma unroll 1
+            for (int i = 0; i < kSpan / (64 * kVec); ++i) {
+                const int e = kVec * (lane + 64 * i);
+                if (e + kVec <= count) {
+                    cpx q[kVec];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int e = lane + 64 * i;
-            if (e < kWindowsPerWave * V && e < left) {
-                const int q = static_cast<int>((static_cast<unsigned>(e) * rcpV) >> 16);
-                const int j = e - q * V;
-                *reinterpret_cast<typename I::W1*>(dst + e) =
-                    I::encode1(region[q * P::kSlot + lds_pad(j)]);
+                    for (int c = 0; c < kVec; ++c) q[c] = value(e + c);
+                    st_nt(reinterpret_cast<W4*>(dst + e), I::encode4(q));
+                } else {
+#pragma unroll
+                    for (int c = 0; c < kVec; ++c)
+                        if (e + c < count)
+                            *reinterpret_cast<W1*>(dst + e + c) = I::encode1(value(e + c));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kSpan / 64; ++i) {
+                const int e = lane + 64 * i;
+                if (e < count) *reinterpret_cast<W1*>(dst + e) = I::encode1(value(e));
             }
         }
     }

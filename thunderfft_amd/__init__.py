@@ -45,6 +45,13 @@ def lib() -> ctypes.CDLL:
             raise ImportError(
                 f"{LIB_PATH} is missing: build it with `python -m thunderfft_amd.build` "
                 "(there is no CPU fallback)")
+        # torch ships its own HIP runtime.  Loaded after this library, it would
+        # be a second runtime in the process, and this library's would find no
+        # device; loaded first, this library binds to torch's (same soname).
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = ctypes.CDLL(LIB_PATH)
         vp = ctypes.c_void_p
         L.thff_version.restype = ctypes.c_int

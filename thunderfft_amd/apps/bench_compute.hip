@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256) void repeat_mfma(const __half2* in, __half2* o
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int n = lane & 15, q = lane >> 4;
     unsigned* region = lds + wave * P::kRegion;
-    f16x8 a[2][2];
+    f16x8 a[2];
     cpx w2[C > 1 ? C - 1 : 1];
     mfma_setup<C, true>(a, w1, w2, tw);
     const long long first = static_cast<long long>(blockIdx.x) * P::kFPB + wave * P::kFPW;
