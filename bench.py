@@ -45,15 +45,18 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target wall time of the CPU baseline sample")
+    ap.add_argument("--sweep", action="store_true",
+                    help="BASELINE config 3 instead: every N at batch 2^26/N, both types and "
+                         "directions; prints one line per case and a JSON summary")
     return ap.parse_args()
 
 
-def time_gpu(T: str, forward: bool, steps: int, warmup: int) -> dict:
+def time_gpu(T: str, forward: bool, steps: int, warmup: int, n: int = N_FFT,
+             batch: int = BATCH) -> dict:
     import torch
 
     import thunderfft_amd as thff
 
-    n, batch = N_FFT, BATCH
     dt = torch.float32 if T == "float" else torch.float16
     elem = 8 if T == "float" else 4
     x = torch.empty(2 * n * batch, dtype=dt, device="cuda")
@@ -78,7 +81,7 @@ def time_gpu(T: str, forward: bool, steps: int, warmup: int) -> dict:
     flops = 5.0 * n * math.log2(n) * batch
     del x, y
     return {
-        "precision": T, "direction": "forward" if forward else "inverse",
+        "precision": T, "direction": "forward" if forward else "inverse", "n": n, "batch": batch,
         "us_per_call": ms * 1e3, "us_per_transform": ms * 1e3 / batch,
         "gflops": flops / (ms * 1e-3) / 1e9,
         "gbps": nbytes / (ms * 1e-3) / 1e9,
@@ -364,6 +367,25 @@ def load_traffic(key: str):
     return int(m.group(1)) if m else None
 
 
+def sweep(a) -> None:
+    """N = 64 ... 4096 at batch 2^26 / N (1 GiB fp32, 512 MiB
+    fp16 moved per launch), float and half, forward and inverse."""
+    import thunderfft_amd as thff
+
+    out = []
+    for T in ("float", "half"):
+        for n in (64, 128, 256, 512, 1024, 2048, 4096):
+            for fwd in (True, False):
+                r = time_gpu(T, fwd, a.steps, a.warmup, n, (1 << 26) // n)
+                out.append({k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()})
+                print(f"[sweep] {T} N={n} batch={(1 << 26) // n} {'forward' if fwd else 'inverse'}: "
+                      f"{r['us_per_call']:.1f} us, {r['gbps']:.0f} GB/s "
+                      f"({r['pct_hbm_peak']:.1f}% of HBM peak), {r['gflops']:.0f} GFLOP/s",
+                      file=sys.stderr, flush=True)
+            thff.ThunderFFTFinalize(T)
+    print(json.dumps({"sweep": out, "steps": a.steps, "warmup": a.warmup}), flush=True)
+
+
 def main():
     a = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -380,6 +402,9 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     thff.lib()
+    if a.sweep:
+        sweep(a)
+        return
     runs = {}
     for T in ("float", "half"):
         for fwd in (True, False):

@@ -297,3 +297,165 @@ c2c_mfma_kernel(const __half2* __restrict__ in,
 }
 
 }  // namespace thff
+
+namespace thff {
+
+// ---------------------------------------------------------------------------
+// half2 C2C of N = 4096 = 16 x 16 x 16 on MFMA, one transform per workgroup
+// tile (4 waves, 16 values per lane).  With n = t0 + 16 t1 + 256 j and
+// k = k1 + 16 k2 + 256 k3 (all digits < 16), t = t0 + 16 t1:
+//   1. DFT16 over j of x[t + 256 j] -> Y1[t][k1].  Wave w, lane (n, q),
+//      block b: t = 64 w + 4 n + b, so the lane's four blocks read four
+//      consecutive values: each of its inputs j = 4 q + e is one 16-byte load
+//      straight from HBM (no staging).  Outputs k1 = q + 4 r.
+//   2. Y1 *= W_4096^(t k1); workgroup exchange through LDS so that wave w'
+//      block b' holds, for k1 = 4 w' + b', the 16 sequences t0 = n (inputs t1)
+//   3. DFT16 over t1 -> Y2[k1][t0][k2], k2 = q + 4 r
+//   4. Y2 *= W_256^(t0 k2); wave-local transpose (as in mfma_fft_staged)
+//   5. DFT16 over t0 -> X[k1 + 16 k2 + 256 k3], k2 = n, k3 = q + 4 r
+// LDS layouts (dwords = half2 values):
+//   exchange: matrix k1 at 272 k1; (t0, t1) at 16 t0 + 4 (((t1 >> 2) + (t0 >> 2)) & 3)
+//             + ((t1 + k1) & 3).  Writers (fixed b, r) have t0 = 4 (n & 3) + b,
+//             t1 = 4 w + (n >> 2), k1 = q + 4 r: banks 16 (b + q) + 4 ((w + n) & 3)
+//             + (((n >> 2) + q) & 3) mod 64, all different.
+//   output staging: out_pad(k) = k + (k >> 6), conflict-free for the stage-3 writes.
+// Three workgroup barriers per tile.  The data is rounded to f16 before stages
+// 2 and 3, as in the two-stage kernel.
+// ---------------------------------------------------------------------------
+struct Mfma4096 {
+    static constexpr int N = 4096;
+    static constexpr int kMatrix = 272;             // exchange matrix stride (dwords)
+    static constexpr int kExchange = 16 * kMatrix;  // 4352
+    static constexpr int kOut = 4096 + 64;          // >= out_pad(4095) + 1 = 4159
+    __device__ static __forceinline__ int out_pad(int k) { return k + (k >> 6); }
+};
+
+template <bool FWD, bool kPrefetch>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c2c_mfma4096_kernel(
+    const __half2* __restrict__ in, __half2* __restrict__ out, int batch,
+    const float2* __restrict__ tw, int tiles_per_block) {
+    using P = Mfma4096;
+    constexpr int N = P::N;
+    __shared__ __align__(16) unsigned xbuf[P::kExchange];
+    __shared__ __align__(16) unsigned obuf[P::kOut];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int n = lane & 15, q = lane >> 4;
+    unsigned* const region = xbuf + 4 * P::kMatrix * wave;  // matrices k1 = 4 wave ... + 3
+
+    f16x8 a[2];
+    dft16_operands<FWD>(a, lane);
+    // Twiddles: W_4096^(t k1), t = 64 wave + 4 n + b, k1 = q + 4 r; W_4096^(16 n k2), k2 = q + 4 r.
+    cpx w1[4][4], w2[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float2 x = tw[((64 * wave + 4 * n + b) * (q + 4 * r)) & (N - 1)];
+            w1[b][r] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+        }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float2 x = tw[(16 * n * (q + 4 * r)) & (N - 1)];
+        w2[r] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+    }
+
+    const long long ntiles = batch;
+    long long tile = static_cast<long long>(blockIdx.x) * tiles_per_block;
+    const long long tile_end = tile + tiles_per_block < ntiles ? tile + tiles_per_block : ntiles;
+    if (tile >= tile_end) return;  // uniform over the workgroup
+
+    // Input j = 4 q + e of the lane's blocks b = 0..3: x[64 wave + 4 n + b + 256 j].
+    auto load = [&](u32x4 (&r)[4], long long tl) {
+        const __half2* src = in + tl * N + 64 * wave + 4 * n + 1024 * q;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = ld_nt(reinterpret_cast<const u32x4*>(src + 256 * e));
+    };
+
+    u32x4 next[4];
+    if constexpr (kPrefetch) load(next, tile);
+    for (; tile < tile_end; ++tile) {
+        u32x4 cur[4];
+        if constexpr (kPrefetch) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cur[i] = next[i];
+            if (tile + 1 < tile_end) load(next, tile + 1);
+        } else {
+            load(cur, tile);
+        }
+
+        // ---- stage 1: DFT16 over j, then W_4096^(t k1) ----
+        cpx y[4][4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            u32x4 x;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = cur[e][b];
+            dft16_block(a, as_f16x8(x), y[b]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) y[b][r] = cmul(y[b][r], w1[b][r]);
+        }
+        __syncthreads();  // every wave is done with the previous tile's exchange buffer
+        // ---- exchange: k1 = q + 4 r, t0 = 4 (n & 3) + b, t1 = 4 wave + (n >> 2) ----
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                xbuf[P::kMatrix * (q + 4 * r) + 16 * (4 * (n & 3) + b) +
+                     4 * ((wave + (n & 3)) & 3) + (((n >> 2) + q) & 3)] = pack_half2(y[b][r]);
+        __syncthreads();
+        // ---- stage 2: block b holds k1 = 4 wave + b; lane (t0 = n, chunk q of t1) ----
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const u32x4 raw = *reinterpret_cast<const u32x4*>(
+                region + P::kMatrix * b + 16 * n + 4 * ((q + (n >> 2)) & 3));
+            u32x4 x;  // t1 = 4 q + e sits at position (e + k1) & 3 = (e + b) & 3
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = raw[(e + b) & 3];
+            dft16_block(a, as_f16x8(x), y[b]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) y[b][r] = cmul(y[b][r], w2[r]);
+        }
+        // ---- wave-local transpose: row 16 b + k2 holds the 16 t0 of (k1, k2) ----
+        wave_lds_sync();
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int k2 = q + 4 * r;
+                region[(16 * b + k2) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] =
+                    pack_half2(y[b][r]);
+            }
+        wave_lds_sync();
+        // ---- stage 3: DFT16 over t0 -> X[k1 + 16 k2 + 256 k3], k2 = n, k3 = q + 4 r ----
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const u32x4 x = *reinterpret_cast<const u32x4*>(
+                region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+            dft16_block(a, as_f16x8(x), y[b]);
+        }
+        __half2* dst = out + tile * N;
+        {
+            // obuf's previous reads ended before this tile's first barrier.  (Writing
+            // the lane's 4 consecutive outputs straight to HBM instead leaves each
+            // 64-byte segment to four waves and measured 4x slower.)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    obuf[P::out_pad(4 * wave + b + 16 * n + 256 * (q + 4 * r))] =
+                        pack_half2(y[b][r]);
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = 4 * tid + 1024 * i;
+                u32x4 v;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) v[c] = obuf[P::out_pad(e + c)];
+                st_nt(reinterpret_cast<u32x4*>(dst + e), v);
+            }
+        }
+    }
+}
+
+}  // namespace thff

@@ -26,13 +26,17 @@ template <int N>
 constexpr LaunchShape launch_shape(int precision) {
     if (precision == 0) return N == 2048 ? LaunchShape{2, true} : LaunchShape{1, false};
     if (N <= 128) return {1, false};
-    if (N == 2048) return {4, true};  // N = 256 ... 2048 run the MFMA kernel
+    if (N == 2048) return {4, true};  // N = 256 ... 4096 run MFMA kernels
+    if (N == 4096) return {4, false};  // the three-stage kernel: its set-up spans 4 tiles
     return {2, N == 1024};
 }
 
-// half2 lengths whose radix-16 stages run on MFMA (fft_mfma.hpp): N = 256*C.
+// half2 lengths whose radix-16 stages run on MFMA (fft_mfma.hpp): N = 256*C
+// (two stages) and N = 4096 (three stages).
 template <int N>
 inline constexpr bool kHalfOnMfma = N >= 256 && N <= 2048;
+template <int N>
+inline constexpr bool kHalfOnMfma3 = N == 4096;
 
 // Only the launch shape in use is instantiated.
 template <class IO, int N, bool FWD>
@@ -49,12 +53,19 @@ void enqueue_mfma(unsigned grid, const __half2* x, __half2* y, int batch, const 
     c2c_mfma_kernel<N / 256, FWD, kPf><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
 }
 
+template <bool FWD>
+void enqueue_mfma4096(unsigned grid, const __half2* x, __half2* y, int batch, const float2* tw,
+                      int tpb, hipStream_t stream) {
+    constexpr bool kPf = launch_shape<4096>(1).prefetch;
+    c2c_mfma4096_kernel<FWD, kPf><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
+}
+
 template <int N>
 hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, int batch,
                       const float2* tw, int num_cus, hipStream_t stream) {
     const LaunchShape shape = launch_shape<N>(precision);
     const bool mfma = precision != 0 && kHalfOnMfma<N>;
-    long long fpb = C2CPlan<N>::kFPB;
+    long long fpb = C2CPlan<N>::kFPB;  // 1 for N = 4096 on either kernel
     if constexpr (kHalfOnMfma<N>)
         if (mfma) fpb = MfmaPlan<N / 256>::kFPB;
     const long long ntiles = (static_cast<long long>(batch) + fpb - 1) / fpb;
@@ -76,6 +87,11 @@ hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, in
                 enqueue_mfma<N, true>(grid, x, y, batch, tw, tpb, stream);
             else
                 enqueue_mfma<N, false>(grid, x, y, batch, tw, tpb, stream);
+        } else if constexpr (kHalfOnMfma3<N>) {
+            if (forward)
+                enqueue_mfma4096<true>(grid, x, y, batch, tw, tpb, stream);
+            else
+                enqueue_mfma4096<false>(grid, x, y, batch, tw, tpb, stream);
         } else if (forward) {
             enqueue<__half2, N, true>(grid, x, y, batch, tw, tpb, stream);
         } else {
