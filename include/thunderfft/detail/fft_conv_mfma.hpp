@@ -1,0 +1,155 @@
+// fft_conv_mfma.hpp -- fused half2 convolutions with the radix-16 stages on
+// MFMA (v_mfma_f32_16x16x32_f16), for N = 256*C, C in {1, 2, 4}.
+//
+// The forward transform (fft_mfma.hpp: stage 1 from LDS, twiddles, DFT_C,
+// LDS transpose, stage 2) leaves lane (n, q) of block b = (f, m) holding
+// Z_f[n + 16 m + 16C (q + 4 r)], r = 0..3.  Read as inputs of the inverse,
+// those are sequence t = 16 m + n (lane n, block m: where the inverse's
+// stage 1 wants it) at inputs j = q + 4 r: the inverse's stage 1 consumes the
+// product straight from registers with column-permuted operands
+// (dft16_operands<..., true>), so the spectra never leave registers.
+#pragma once
+
+#include "fft_conv.hpp"
+#include "fft_mfma.hpp"
+
+namespace thff {
+
+// Two rows of halves (8 per 16-byte word) <-> 8 half2 (row 0 = real part).
+__device__ __forceinline__ void interleave_rows(u32x4 r0, u32x4 r1, u32x4& lo, u32x4& hi) {
+    const unsigned a[4] = {r0.x, r0.y, r0.z, r0.w}, b[4] = {r1.x, r1.y, r1.z, r1.w};
+    unsigned z[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        z[2 * i] = (a[i] & 0xffffu) | (b[i] << 16);
+        z[2 * i + 1] = (a[i] >> 16) | (b[i] & 0xffff0000u);
+    }
+    lo = u32x4{z[0], z[1], z[2], z[3]};
+    hi = u32x4{z[4], z[5], z[6], z[7]};
+}
+__device__ __forceinline__ void split_rows(u32x4 lo, u32x4 hi, u32x4& r0, u32x4& r1) {
+    const unsigned z[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    unsigned a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        a[i] = (z[2 * i] & 0xffffu) | (z[2 * i + 1] << 16);
+        b[i] = (z[2 * i] >> 16) | (z[2 * i + 1] & 0xffff0000u);
+    }
+    r0 = u32x4{a[0], a[1], a[2], a[3]};
+    r1 = u32x4{b[0], b[1], b[2], b[3]};
+}
+
+// Real-input fused convolution (conv1d_real_kernel's contract, fp16 storage)
+// on MFMA: complex transform tau = p * D + d carries rows (2p, d) and
+// (2p + 1, d) as real and imaginary parts; a wave owns kFPW = 4/C transforms
+// (1024 complex values), a tile is 4 waves.  Lane l moves 8 values of both
+// rows per 16-byte step: values e = 8 l + 512 i (i = 0, 1) of the wave.
+// C = 1 (four transforms per wave, each with its own channel) needs a few
+// more registers than 4 waves per SIMD leave without spilling.
+template <int C>
+inline constexpr int kConvMfmaMinWavesPerEU = C == 1 ? 3 : 4;
+
+template <int C>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kConvMfmaMinWavesPerEU<C>))) void
+conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__ spectrum,
+                        __half* __restrict__ y, int batch, int channels,
+                        const float2* __restrict__ tw, int tiles_per_block) {
+    static_assert(C <= 4, "one 1024-value wave span per tile step");
+    using P = MfmaPlan<C>;
+    constexpr int N = P::N;
+    constexpr int kB = P::kBlocks;
+    __shared__ unsigned lds[4 * P::kRegion];
+    __shared__ cpx w1[P::kTw1];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int n = lane & 15, q = lane >> 4;
+    unsigned* region = lds + wave * P::kRegion;
+
+    f16x8 a[2], ai[2], ai_regs[2];
+    cpx w2[C > 1 ? C - 1 : 1];
+    mfma_setup<C, true>(a, w1, w2, tw);  // forward operands and twiddles
+    dft16_operands<false>(ai, lane);
+    dft16_operands<false, true>(ai_regs, lane);
+
+    const long long pairs = (static_cast<long long>(batch) + 1) / 2;
+    const long long transforms = pairs * channels;
+    const long long ntiles = (transforms + P::kFPB - 1) / P::kFPB;
+    long long tile, tile_end;
+    block_tiles(ntiles, tiles_per_block, tile, tile_end);
+
+    for (; tile < tile_end; ++tile) {
+        // Rows of this wave's transforms, as element offsets (-1: none).
+        long long base0[2], base1[2];
+        int chan[P::kFPW];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int e = 8 * lane + 512 * i;
+            const long long tau = tile * P::kFPB + wave * P::kFPW + e / N;
+            const long long p = tau / channels, d = tau - p * channels;
+            const int k = e % N;
+            base0[i] = tau < transforms ? (2 * p * channels + d) * N + k : -1;
+            base1[i] = tau < transforms && 2 * p + 1 < batch ? ((2 * p + 1) * channels + d) * N + k
+                                                             : -1;
+        }
+#pragma unroll
+        for (int f = 0; f < P::kFPW; ++f) {
+            const long long tau = tile * P::kFPB + wave * P::kFPW + f;
+            chan[f] = tau < transforms ? static_cast<int>(tau % channels) : 0;
+        }
+        u32x4 r0[2], r1[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            r0[i] = base0[i] >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + base0[i])) : u32x4{};
+            r1[i] = base1[i] >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + base1[i])) : u32x4{};
+        }
+        wave_lds_sync();  // the previous tile's output reads are done
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int e = 8 * lane + 512 * i;
+            u32x4 lo, hi;
+            interleave_rows(r0[i], r1[i], lo, hi);
+            *reinterpret_cast<u32x4*>(region + P::in_pad(e)) = lo;
+            *reinterpret_cast<u32x4*>(region + P::in_pad(e + 4)) = hi;
+        }
+        wave_lds_sync();
+
+        cpx v[kB][4];
+        mfma_stage1_lds<C>(region, a, lane, v);
+        mfma_steps2to6<C, true>(region, a, w1, w2, lane, v);
+        // ---- product: block (f, m), lane (n, q): bin k = n + 16 m + 16C (q + 4 r) ----
+#pragma unroll
+        for (int b = 0; b < kB; ++b) {
+            const float2* hs = spectrum + static_cast<long long>(chan[b / C]) * N + n + 16 * (b % C) +
+                               P::kM * q;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float2 hk = hs[P::kM * 4 * r];
+                v[b][r] = cmul(v[b][r], cpx{hk.x, hk.y});
+            }
+        }
+        // ---- inverse, stage 1 straight from the registers ----
+        mfma_stage1_regs<C>(ai_regs, v);
+        mfma_steps2to6<C, false, true>(region, ai, w1, w2, lane, v);
+        // ---- real part -> row 2p, imaginary part -> row 2p + 1 ----
+        wave_lds_sync();
+#pragma unroll
+        for (int b = 0; b < kB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                region[P::out_pad((b / C) * N + n + 16 * (b % C) + P::kM * (q + 4 * r))] =
+                    pack_half2(v[b][r]);
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int e = 8 * lane + 512 * i;
+            const u32x4 lo = *reinterpret_cast<const u32x4*>(region + P::out_pad(e));
+            const u32x4 hi = *reinterpret_cast<const u32x4*>(region + P::out_pad(e + 4));
+            u32x4 o0, o1;
+            split_rows(lo, hi, o0, o1);
+            if (base0[i] >= 0) st_nt(reinterpret_cast<u32x4*>(y + base0[i]), o0);
+            if (base1[i] >= 0) st_nt(reinterpret_cast<u32x4*>(y + base1[i]), o1);
+        }
+    }
+}
+
+}  // namespace thff

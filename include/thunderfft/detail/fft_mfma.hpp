@@ -54,7 +54,11 @@ __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
 // A-operand registers of the DFT16 matrix for this lane: [half].
 // Row m of half h is output k = m/4 + 4*(2h + (m%4)/2), part (m%4)%2;
 // column k' is input j = k'/2, part k'%2.
-template <bool FWD>
+// With kInterleaved, lane group q of the data operand holds inputs
+// j = q + 4 e (e = 0..3) instead of 4 q + e: the columns are permuted to match,
+// so a transform can consume another transform's output registers (whose
+// lane group q holds outputs q + 4 r) without moving them.
+template <bool FWD, bool kInterleaved = false>
 __device__ __forceinline__ void dft16_operands(f16x8 (&a)[2], int lane) {
     const int m = lane & 15, q = lane >> 4;
     const int gq = m >> 2, i = m & 3;
@@ -65,7 +69,8 @@ __device__ __forceinline__ void dft16_operands(f16x8 (&a)[2], int lane) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int kk = 8 * q + e;
-            const int j = kk >> 1, p = kk & 1;
+            const int j = kInterleaved ? (kk >> 3) + 4 * ((kk >> 1) & 3) : kk >> 1;
+            const int p = kk & 1;
             const int ang = (j * k) & 15;
             const float c = kCos16[ang];
             const float s = FWD ? -kSin16[ang] : kSin16[ang];
@@ -146,27 +151,52 @@ __device__ __forceinline__ void mfma_setup(f16x8 (&a)[2], cpx* w1, cpx* w2,
     __syncthreads();
 }
 
-// Steps 1-6 for the kFPW transforms a wave has staged in `region` (natural
-// order at MfmaPlan<C>::in_pad positions); on return lane (n = k1, q) holds,
-// for block b = (f, m), y[b][r] = X_f[k1 + 16 m + 16C (q + 4 r)].  `region`
-// is overwritten (the transpose of step 5).
-template <int C, bool FWD>
-__device__ __forceinline__ void mfma_fft_staged(unsigned* region, const f16x8 (&a)[2],
-                                                const cpx* w1, const cpx* w2, int lane,
-                                                cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
+// Step 1 from LDS: the kFPW transforms a wave has staged in `region` (natural
+// order at MfmaPlan<C>::in_pad positions); block b = (f, c) gets the DFT16
+// over j of x_f[16 c + n + 16C j] -> y[b][r] = Y[k1 = q + 4 r].
+template <int C>
+__device__ __forceinline__ void mfma_stage1_lds(const unsigned* region, const f16x8 (&a)[2],
+                                                int lane, cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
     using P = MfmaPlan<C>;
-    constexpr int N = P::N;
-    constexpr int kB = P::kBlocks;
     const int n = lane & 15, q = lane >> 4;
-    // ---- step 1: block b = (transform f, column block c): DFT16 over j ----
 #pragma unroll
-    for (int b = 0; b < kB; ++b) {
-        const int base = (b / C) * N + 16 * (b % C) + n;
+    for (int b = 0; b < P::kBlocks; ++b) {
+        const int base = (b / C) * P::N + 16 * (b % C) + n;
         u32x4 x;
 #pragma unroll
         for (int e = 0; e < 4; ++e) x[e] = region[P::in_pad(base + P::kM * (4 * q + e))];
         dft16_block(a, as_f16x8(x), y[b]);
     }
+}
+
+// Step 1 from registers: y[b][r] holds z_f[16 c + n + 16C (q + 4 r)] (the
+// layout a forward transform leaves), `a` built with kInterleaved.
+template <int C>
+__device__ __forceinline__ void mfma_stage1_regs(const f16x8 (&a)[2],
+                                                 cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
+#pragma unroll
+    for (int b = 0; b < MfmaPlan<C>::kBlocks; ++b) {
+        u32x4 x;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[r] = pack_half2(y[b][r]);
+        dft16_block(a, as_f16x8(x), y[b]);
+    }
+}
+
+// Steps 2-6 on the stage-1 outputs: twiddle, DFT_C over c, twiddle, LDS
+// transpose through `region` (overwritten), DFT16 over n.  The twiddle
+// tables hold the direction TW_FWD (w1 = [c][r][lane] in LDS, w2 in
+// registers); a transform of the other direction uses their conjugates.
+// On return lane (n = k1, q) holds, for block b = (f, m),
+// y[b][r] = X_f[k1 + 16 m + 16C (q + 4 r)].
+template <int C, bool FWD, bool TW_FWD = FWD>
+__device__ __forceinline__ void mfma_steps2to6(unsigned* region, const f16x8 (&a)[2],
+                                               const cpx* w1, const cpx* w2, int lane,
+                                               cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
+    using P = MfmaPlan<C>;
+    constexpr int kB = P::kBlocks;
+    constexpr bool kConj = FWD != TW_FWD;
+    const int n = lane & 15, q = lane >> 4;
     // ---- steps 2-4: twiddle, DFT_C over c, twiddle ----
 #pragma unroll
     for (int f = 0; f < P::kFPW; ++f)
@@ -174,11 +204,14 @@ __device__ __forceinline__ void mfma_fft_staged(unsigned* region, const f16x8 (&
         for (int r = 0; r < 4; ++r) {
             cpx v[C];
 #pragma unroll
-            for (int c = 0; c < C; ++c) v[c] = cmul(y[f * C + c][r], w1[(c * 4 + r) * 64 + lane]);
+            for (int c = 0; c < C; ++c) {
+                const cpx w = w1[(c * 4 + r) * 64 + lane];
+                v[c] = kConj ? cmulc(y[f * C + c][r], w) : cmul(y[f * C + c][r], w);
+            }
             Dft<C, FWD>::run(v);
             y[f * C][r] = v[0];
 #pragma unroll
-            for (int m = 1; m < C; ++m) y[f * C + m][r] = cmul(v[m], w2[m - 1]);
+            for (int m = 1; m < C; ++m) y[f * C + m][r] = kConj ? cmulc(v[m], w2[m - 1]) : cmul(v[m], w2[m - 1]);
         }
     // ---- step 5: transpose: row 16b + k1 holds the 16 inputs n of
     // sequence (k1, m) of block b = (f, m); its 4-value chunks are rotated
@@ -199,6 +232,15 @@ __device__ __forceinline__ void mfma_fft_staged(unsigned* region, const f16x8 (&
             region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
         dft16_block(a, as_f16x8(x), y[b]);
     }
+}
+
+// Steps 1-6 for the kFPW transforms a wave has staged in `region`.
+template <int C, bool FWD>
+__device__ __forceinline__ void mfma_fft_staged(unsigned* region, const f16x8 (&a)[2],
+                                                const cpx* w1, const cpx* w2, int lane,
+                                                cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
+    mfma_stage1_lds<C>(region, a, lane, y);
+    mfma_steps2to6<C, FWD>(region, a, w1, w2, lane, y);
 }
 
 // Batched C2C of half2 signals of N = 256*C on MFMA (C = 4 is N = 1024 as
