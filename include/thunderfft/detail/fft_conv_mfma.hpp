@@ -153,3 +153,124 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
 }
 
 }  // namespace thff
+
+namespace thff {
+
+// Complex fused convolution (conv1d_kernel's contract, half2 storage) on
+// MFMA: y[b] = IFFT(FFT(x[b]) * FFT(h[b or 0])) / N.  A wave owns kFPW
+// transforms (1024 values for C <= 4, one transform of 2048 for C = 8); the
+// filter spectrum is kept packed as half2 between the transforms.
+template <int C>
+inline constexpr int kConv1dMfmaMinWavesPerEU = C <= 4 ? 3 : 2;
+
+template <int C, bool kPerSignal>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kConv1dMfmaMinWavesPerEU<C>))) void
+conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
+                   __half2* __restrict__ y, int batch, const float2* __restrict__ tw,
+                   int tiles_per_block) {
+    using P = MfmaPlan<C>;
+    constexpr int N = P::N;
+    constexpr int kB = P::kBlocks;
+    constexpr int kRaw = P::kVals / 4;  // 16-byte loads per lane
+    __shared__ unsigned lds[4 * P::kRegion];
+    __shared__ cpx w1[P::kTw1];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int n = lane & 15, q = lane >> 4;
+    unsigned* region = lds + wave * P::kRegion;
+    constexpr float kScale = 1.0f / N;
+
+    f16x8 a[2], ai[2], ai_regs[2];
+    cpx w2[C > 1 ? C - 1 : 1];
+    mfma_setup<C, true>(a, w1, w2, tw);
+    dft16_operands<false>(ai, lane);
+    dft16_operands<false, true>(ai_regs, lane);
+
+    const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
+    long long tile, tile_end;
+    block_tiles(ntiles, tiles_per_block, tile, tile_end);
+
+    // Valid values (0..kWaveVals) of this wave's transforms in tile tl.
+    auto valid = [&](long long tl) {
+        const long long v = (static_cast<long long>(batch) - tl * P::kFPB - wave * P::kFPW) * N;
+        return v <= 0 ? 0 : (v >= P::kWaveVals ? P::kWaveVals : static_cast<int>(v));
+    };
+    // Stage `src` (this wave's kWaveVals values, nv of them valid) and transform it.
+    auto forward = [&](const __half2* src, int nv, cpx (&v)[kB][4]) {
+        u32x4 raw[kRaw];
+#pragma unroll
+        for (int i = 0; i < kRaw; ++i) {
+            const int e = 4 * lane + 256 * i;
+            raw[i] = e < nv ? ld_nt(reinterpret_cast<const u32x4*>(src + e)) : u32x4{};
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < kRaw; ++i)
+            *reinterpret_cast<u32x4*>(region + P::in_pad(4 * lane + 256 * i)) = raw[i];
+        wave_lds_sync();
+        mfma_stage1_lds<C>(region, a, lane, v);
+        mfma_steps2to6<C, true>(region, a, w1, w2, lane, v);
+    };
+
+    unsigned hp[kB][4];  // FFT(h) / N, packed half2
+    auto keep = [&](const cpx (&v)[kB][4]) {
+#pragma unroll
+        for (int b = 0; b < kB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) hp[b][r] = pack_half2({v[b][r].re * kScale, v[b][r].im * kScale});
+    };
+    if constexpr (!kPerSignal) {
+        // Every transform of the wave is the shared filter: stage it kFPW times.
+        cpx v[kB][4];
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < kRaw; ++i) {
+            const int e = 4 * lane + 256 * i;
+            *reinterpret_cast<u32x4*>(region + P::in_pad(e)) =
+                ld_nt(reinterpret_cast<const u32x4*>(h + e % N));
+        }
+        wave_lds_sync();
+        mfma_stage1_lds<C>(region, a, lane, v);
+        mfma_steps2to6<C, true>(region, a, w1, w2, lane, v);
+        keep(v);
+    }
+
+    for (; tile < tile_end; ++tile) {
+        const int nv = valid(tile);
+        const long long off = (tile * P::kFPB + wave * P::kFPW) * N;
+        cpx v[kB][4];
+        if constexpr (kPerSignal) {
+            forward(h + off, nv, v);
+            keep(v);
+        }
+        forward(x + off, nv, v);
+#pragma unroll
+        for (int b = 0; b < kB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float2 hk = __half22float2(__builtin_bit_cast(__half2, hp[b][r]));
+                v[b][r] = cmul(v[b][r], cpx{hk.x, hk.y});
+            }
+        mfma_stage1_regs<C>(ai_regs, v);
+        mfma_steps2to6<C, false, true>(region, ai, w1, w2, lane, v);
+        // ---- store: block (f, m), lane (n, q) holds y_f[n + 16 m + 16C (q + 4 r)] ----
+        wave_lds_sync();
+#pragma unroll
+        for (int b = 0; b < kB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                region[P::out_pad((b / C) * N + n + 16 * (b % C) + P::kM * (q + 4 * r))] =
+                    pack_half2(v[b][r]);
+        wave_lds_sync();
+        __half2* dst = y + off;
+#pragma unroll
+        for (int i = 0; i < kRaw; ++i) {
+            const int e = 4 * lane + 256 * i;
+            if (e < nv)
+                st_nt(reinterpret_cast<u32x4*>(dst + e),
+                      *reinterpret_cast<const u32x4*>(region + P::out_pad(e)));
+        }
+    }
+}
+
+}  // namespace thff
