@@ -214,7 +214,15 @@ def test_full_size_impulse_rolls(T, n, batch, channels):
     idx = (np.arange(n)[None, :] - shifts[:, None]) % n  # y[k] = x[(k - s) mod N]
     expect = np.take_along_axis(x, np.broadcast_to(idx, x.shape), axis=-1)
     err = np.abs(y - expect)
-    tol = (1e-5 if T == "float" else 2.0 ** -11) * np.abs(expect) + 2e-6
-    label = f"{T} N={n} B={batch} D={channels}: max_err={err.max():.3e}"
+    rel = float(np.linalg.norm((y - expect).ravel()) / np.linalg.norm(expect.ravel()))
+    label = f"{T} N={n} B={batch} D={channels}: max_err={err.max():.3e} rel_l2={rel:.3e}"
     print(label, flush=True)
-    assert np.all(np.isfinite(y)) and np.all(err <= tol), label
+    assert np.all(np.isfinite(y)), label
+    if T == "float":
+        # fp32 between the transforms: every element within fp32 rounding
+        assert np.all(err <= 1e-5 * np.abs(expect) + 2e-6), label
+    else:
+        # fp16 N = 256 ... 1024 run on MFMA with f16 data between the stages:
+        # errors are spread evenly over a signal, so bound them against the
+        # signal scale (|x| <= 1 here); a wrong shift or channel is O(1)
+        assert rel <= 1e-3 and err.max() <= 5e-3, label
