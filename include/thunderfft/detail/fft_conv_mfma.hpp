@@ -74,8 +74,11 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
     const long long pairs = (static_cast<long long>(batch) + 1) / 2;
     const long long transforms = pairs * channels;
     const long long ntiles = (transforms + P::kFPB - 1) / P::kFPB;
-    long long tile, tile_end;
-    block_tiles(ntiles, tiles_per_block, tile, tile_end);
+    long long tile, tile_end;  // tiles_per_block = 0: balanced shares of a device-sized grid
+    if (tiles_per_block > 0)
+        block_tiles(ntiles, tiles_per_block, tile, tile_end);
+    else
+        grid_tiles(ntiles, tile, tile_end);
 
     for (; tile < tile_end; ++tile) {
         // Rows of this wave's transforms, as element offsets (-1: none).
@@ -187,8 +190,11 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
     dft16_operands<false, true>(ai_regs, lane);
 
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
-    long long tile, tile_end;
-    block_tiles(ntiles, tiles_per_block, tile, tile_end);
+    long long tile, tile_end;  // tiles_per_block = 0: balanced shares of a device-sized grid
+    if (tiles_per_block > 0)
+        block_tiles(ntiles, tiles_per_block, tile, tile_end);
+    else
+        grid_tiles(ntiles, tile, tile_end);
 
     // Valid values (0..kWaveVals) of this wave's transforms in tile tl.
     auto valid = [&](long long tl) {
@@ -269,6 +275,186 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
             if (e < nv)
                 st_nt(reinterpret_cast<u32x4*>(dst + e),
                       *reinterpret_cast<const u32x4*>(region + P::out_pad(e)));
+        }
+    }
+}
+
+}  // namespace thff
+
+namespace thff {
+
+// Real-input fused convolution at N = 4096 (the reference's default length)
+// on the three-stage MFMA transform of c2c_mfma4096_kernel, one complex
+// transform (two real rows) per workgroup tile.
+//   forward: stage 1 over j for t = 64 w + 4 n + b (inputs straight from the
+//            two rows: 4 consecutive values of each, interleaved into half2),
+//            exchange, stage 2, transpose, stage 3 -> lane (n, q) of block b
+//            holds Z[k1 + 16 k2 + 256 k3], k1 = 4 w + b, k2 = n, k3 = q + 4 r;
+//   product with the channel's spectrum;
+//   inverse: stage 1 straight from those registers (sequence t' = k1 + 16 k2
+//            = 4 w + b + 16 n, inputs k3 = q + 4 r: interleaved operands),
+//            exchange with t0' = 4 w + b, t1' = n, stage 2, transpose,
+//            stage 3 -> y[k1' + 16 k2' + 256 k3'], then staged output split
+//            back into the two rows.
+// Exchange element (k1, t0, t1) sits at 272 k1 + 16 t0 + 4 (((t1 >> 2) +
+// (t0 >> 2)) & 3) + ((t1 + k1) & 3); for the inverse's writers (fixed b, r)
+// the banks are 16 (b + q) + 4 (((n >> 2) + w) & 3) + (((n & 3) + q) & 3)
+// mod 64, all different, as for the forward ones.
+__device__ __forceinline__ int xaddr4096(int k1, int t0, int t1) {
+    return Mfma4096::kMatrix * k1 + 16 * t0 + 4 * (((t1 >> 2) + (t0 >> 2)) & 3) + ((t1 + k1) & 3);
+}
+
+template <int N>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void
+conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restrict__ spectrum,
+                            __half* __restrict__ y, int batch, int channels,
+                            const float2* __restrict__ tw, int tiles_per_block) {
+    using P = Mfma4096;
+    static_assert(N == P::N, "the three-stage transform is N = 4096");
+    __shared__ __align__(16) unsigned xbuf[P::kExchange];
+    __shared__ __align__(16) unsigned obuf[P::kOut];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int n = lane & 15, q = lane >> 4;
+    unsigned* const region = xbuf + 4 * P::kMatrix * wave;
+
+    f16x8 a[2], ai[2], ai_regs[2];
+    dft16_operands<true>(a, lane);
+    dft16_operands<false>(ai, lane);
+    dft16_operands<false, true>(ai_regs, lane);
+    // Twiddles (positive angles; the forward conjugates): stage 1 -> 2
+    // W^(t k1) for the forward's t = 64 w + 4 n + b and the inverse's
+    // t' = 4 w + b + 16 n; stage 2 -> 3 W^(16 n k2), k = q + 4 r.
+    cpx w1f[4][4], w1i[4][4], w2[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float2 f = tw[((64 * wave + 4 * n + b) * (q + 4 * r)) & (N - 1)];
+            const float2 g = tw[((4 * wave + b + 16 * n) * (q + 4 * r)) & (N - 1)];
+            w1f[b][r] = cpx{f.x, -f.y};
+            w1i[b][r] = cpx{g.x, g.y};
+        }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float2 g = tw[(16 * n * (q + 4 * r)) & (N - 1)];
+        w2[r] = cpx{g.x, g.y};
+    }
+
+    // tiles_per_block = 0: the grid is sized to the device and the transforms
+    // are shared out evenly (grid_tiles); otherwise contiguous runs.
+    const long long transforms = (static_cast<long long>(batch) + 1) / 2 * channels;
+    long long tile, tile_end;
+    if (tiles_per_block > 0)
+        block_tiles(transforms, tiles_per_block, tile, tile_end);
+    else
+        grid_tiles(transforms, tile, tile_end);
+
+    // Stage 2 of either direction, the wave-local transpose and stage 3.
+    auto stages23 = [&](cpx (&v)[4][4], const f16x8 (&op)[2], bool conj_w2) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const u32x4 raw = *reinterpret_cast<const u32x4*>(
+                region + P::kMatrix * b + 16 * n + 4 * ((q + (n >> 2)) & 3));
+            u32x4 xv;  // t1 = 4 q + e sits at position (e + k1) & 3 = (e + b) & 3
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[e] = raw[(e + b) & 3];
+            dft16_block(op, as_f16x8(xv), v[b]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[b][r] = conj_w2 ? cmulc(v[b][r], w2[r]) : cmul(v[b][r], w2[r]);
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                region[(16 * b + q + 4 * r) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] =
+                    pack_half2(v[b][r]);
+        wave_lds_sync();
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const u32x4 xv = *reinterpret_cast<const u32x4*>(
+                region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+            dft16_block(op, as_f16x8(xv), v[b]);
+        }
+    };
+
+    for (; tile < tile_end; ++tile) {
+        const long long p = tile / channels, d = tile - p * channels;
+        const long long row0 = (2 * p * channels + d) * N;
+        const long long row1 = 2 * p + 1 < batch ? ((2 * p + 1) * channels + d) * N : -1;
+        // ---- stage-1 inputs: values 64 w + 4 n + 1024 q + 256 e .. + 3 of both rows ----
+        u32x4 z[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int k = 64 * wave + 4 * n + 1024 * q + 256 * e;
+            const u32x2 a0 = ld_nt(reinterpret_cast<const u32x2*>(x + row0 + k));
+            const u32x2 a1 = row1 >= 0 ? ld_nt(reinterpret_cast<const u32x2*>(x + row1 + k)) : u32x2{};
+            z[e] = u32x4{(a0.x & 0xffffu) | (a1.x << 16), (a0.x >> 16) | (a1.x & 0xffff0000u),
+                         (a0.y & 0xffffu) | (a1.y << 16), (a0.y >> 16) | (a1.y & 0xffff0000u)};
+        }
+        cpx v[4][4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            u32x4 xv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[e] = z[e][b];
+            dft16_block(a, as_f16x8(xv), v[b]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], w1f[b][r]);
+        }
+        __syncthreads();  // every wave is done with the previous tile's exchange buffer
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                xbuf[xaddr4096(q + 4 * r, 4 * (n & 3) + b, 4 * wave + (n >> 2))] = pack_half2(v[b][r]);
+        __syncthreads();
+        stages23(v, a, true);
+        // ---- product: bin k = 4 w + b + 16 n + 256 (q + 4 r) ----
+        const float2* hs = spectrum + d * N + 4 * wave + 16 * n + 256 * q;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float2 hk = hs[b + 1024 * r];
+                v[b][r] = cmul(v[b][r], cpx{hk.x, hk.y});
+            }
+        // ---- inverse stage 1 from the registers, then W^(t' k1') ----
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            u32x4 xv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) xv[r] = pack_half2(v[b][r]);
+            dft16_block(ai_regs, as_f16x8(xv), v[b]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], w1i[b][r]);
+        }
+        __syncthreads();  // every wave's forward stage-3 reads are done
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                xbuf[xaddr4096(q + 4 * r, 4 * wave + b, n)] = pack_half2(v[b][r]);
+        __syncthreads();
+        stages23(v, ai, false);
+        // ---- output: y[k1 + 16 k2 + 256 k3], k1 = 4 w + b, k2 = n, k3 = q + 4 r ----
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                obuf[P::out_pad(4 * wave + b + 16 * n + 256 * (q + 4 * r))] = pack_half2(v[b][r]);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int k = 4 * tid + 1024 * i;
+            unsigned zz[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) zz[c] = obuf[P::out_pad(k + c)];
+            const u32x2 o0{(zz[0] & 0xffffu) | (zz[1] << 16), (zz[2] & 0xffffu) | (zz[3] << 16)};
+            const u32x2 o1{(zz[0] >> 16) | (zz[1] & 0xffff0000u), (zz[2] >> 16) | (zz[3] & 0xffff0000u)};
+            st_nt(reinterpret_cast<u32x2*>(y + row0 + k), o0);
+            if (row1 >= 0) st_nt(reinterpret_cast<u32x2*>(y + row1 + k), o1);
         }
     }
 }

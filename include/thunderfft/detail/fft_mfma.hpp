@@ -277,8 +277,11 @@ c2c_mfma_kernel(const __half2* __restrict__ in,
     mfma_setup<C, FWD>(a, w1, w2, tw);
 
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
-    long long tile = static_cast<long long>(blockIdx.x) * tiles_per_block;
-    const long long tile_end = tile + tiles_per_block < ntiles ? tile + tiles_per_block : ntiles;
+    long long tile, tile_end;  // tiles_per_block = 0: balanced shares of a device-sized grid
+    if (tiles_per_block > 0)
+        block_tiles(ntiles, tiles_per_block, tile, tile_end);
+    else
+        grid_tiles(ntiles, tile, tile_end);
     if (tile >= tile_end) return;  // uniform over the workgroup
 
     // Valid values (0..kWaveVals) of this wave's kFPW transforms in tile tl.
@@ -402,9 +405,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
         w2[r] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
     }
 
-    const long long ntiles = batch;
-    long long tile = static_cast<long long>(blockIdx.x) * tiles_per_block;
-    const long long tile_end = tile + tiles_per_block < ntiles ? tile + tiles_per_block : ntiles;
+    // tiles_per_block = 0: the grid is sized to the device and the batch is
+    // shared out evenly (grid_tiles); otherwise contiguous runs of that many.
+    long long tile, tile_end;
+    if (tiles_per_block > 0)
+        block_tiles(batch, tiles_per_block, tile, tile_end);
+    else
+        grid_tiles(batch, tile, tile_end);
     if (tile >= tile_end) return;  // uniform over the workgroup
 
     // Input j = 4 q + e of the lane's blocks b = 0..3: x[64 wave + 4 n + b + 256 j].

@@ -269,4 +269,13 @@ __device__ __forceinline__ void block_tiles(long long ntiles, int tiles_per_bloc
     end = first + tiles_per_block < ntiles ? first + tiles_per_block : ntiles;
 }
 
+// Balanced share of ntiles over the grid: [b T / G, (b + 1) T / G), so the
+// workgroups' tile counts differ by at most one (for grids sized to the
+// device rather than to the batch).
+__device__ __forceinline__ void grid_tiles(long long ntiles, long long& first, long long& end) {
+    const long long g = gridDim.x, b = blockIdx.x;
+    first = b * ntiles / g;
+    end = (b + 1) * ntiles / g;
+}
+
 }  // namespace thff

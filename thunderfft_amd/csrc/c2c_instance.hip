@@ -28,7 +28,7 @@ constexpr LaunchShape launch_shape(int precision) {
     if (precision == 0) return N == 2048 ? LaunchShape{2, true} : LaunchShape{1, false};
     if (N <= 128) return {1, false};
     if (N == 2048) return {4, true};  // N = 256 ... 4096 run MFMA kernels
-    if (N == 4096) return {4, false};  // the three-stage kernel: its set-up spans 4 tiles
+    if (N == 4096) return {0, false};  // the three-stage kernel: grid sized to the device
     return {2, N == 1024};
 }
 
@@ -71,8 +71,18 @@ hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, in
         if (mfma) fpb = MfmaPlan<N / 256>::kFPB;
     const long long ntiles = (static_cast<long long>(batch) + fpb - 1) / fpb;
     // Small batches spread one tile per workgroup over the whole device.
-    const int tpb = ntiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? shape.tiles : 1;
-    const unsigned grid = static_cast<unsigned>((ntiles + tpb - 1) / tpb);
+    int tpb = ntiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? shape.tiles : 1;
+    unsigned grid = static_cast<unsigned>((ntiles + tpb - 1) / tpb);
+    if constexpr (kHalfOnMfma3<N>) {
+        // The three-stage kernel: 2 workgroups per CU sharing the batch evenly
+        // (tpb = 0) measured 99 us against 105-107 us for 4, 8 or 16 tiles per
+        // workgroup (2^26 values, MI355X); its set-up is the heaviest.
+        if (precision != 0) {
+            const long long cap = 2LL * (num_cus > 0 ? num_cus : 256);
+            grid = static_cast<unsigned>(ntiles < cap ? ntiles : cap);
+            tpb = 0;
+        }
+    }
     if (precision == 0) {
         const auto* x = static_cast<const float2*>(in);
         auto* y = static_cast<float2*>(out);
@@ -178,6 +188,19 @@ hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectr
             conv1d_real_mfma_kernel<N / 256><<<grid, 256, 0, stream>>>(
                 static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch, channels,
                 tw, tpb);
+            return hipGetLastError();
+        }
+    }
+    // fp16 N = 4096: the three-stage MFMA transform, both directions.
+    if constexpr (N == 4096) {
+        if (precision != 0) {
+            // 2 workgroups per CU sharing the transforms evenly: 87-90 us
+            // against 107 us for 4 tiles per workgroup (2^26 samples, MI355X).
+            const long long cap = 2LL * (num_cus > 0 ? num_cus : 256);
+            const unsigned grid = static_cast<unsigned>(transforms < cap ? transforms : cap);
+            conv1d_real_mfma4096_kernel<N><<<grid, 256, 0, stream>>>(
+                static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch, channels,
+                tw, 0);
             return hipGetLastError();
         }
     }
