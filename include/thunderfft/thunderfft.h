@@ -64,7 +64,10 @@ int thff_finalize(int precision);
  * Argument checks in the reference's order, all before any HIP call:
  *   unsupported precision or n -> THFF_EINVAL (a static_assert there);
  *   batch < 0 -> THFF_EINVAL; batch == 0 -> THFF_OK without touching the
- *   pointers; null d_input or d_output, or d_input == d_output -> THFF_EINVAL.
+ *   pointers; null d_input or d_output, or d_input == d_output -> THFF_EINVAL;
+ *   a buffer not on a 16-byte boundary -> THFF_EINVAL (the kernels move
+ *   16-byte vectors; the reference has no such check, and any hipMalloc'd
+ *   pointer or offset of whole transforms meets it).
  * Requires thff_initialize(precision, n) on the current device (THFF_EIO
  * otherwise).  Synchronises `stream` before returning, like the reference. */
 int thff_global(int precision, int n, int forward, const void* d_input, void* d_output,

@@ -85,7 +85,8 @@ inline const float2* ThunderFFT_twiddle_table() {
 
 // Batched unnormalized out-of-place C2C FFT of `batch` natural-order signals
 // of N values (signal j at offset j*N).  forward = exp(-2*pi*i*k/N).
-// batch < 0, null or identical pointers throw std::invalid_argument; batch 0
+// batch < 0, null, identical or not 16-byte aligned pointers throw
+// std::invalid_argument; batch 0
 // is a no-op.  Synchronises `stream` before returning.
 template <typename T, int N, bool forward = true>
 inline void ThunderFFT_global(vec2_t<T>* d_input, vec2_t<T>* d_output, int batch,

@@ -155,3 +155,20 @@ def test_conv1d_valid_argument_checks():
         v("half", 16, 100, 36, 9, 48, 1)    # fp32 complex taps not 8-byte aligned
     with pytest.raises(ValueError):
         v("double", 16, 100, 32, 9, 48, 1)
+
+
+def test_misaligned_buffers_rejected():
+    """The kernels move 16-byte vectors, so every entry point rejects buffers
+    that do not start on a 16-byte boundary (THFF_EINVAL, before any HIP
+    call).  The reference takes any pointer; hipMalloc'd buffers and offsets
+    of whole transforms are always aligned."""
+    for T in ("float", "half"):
+        for x, y in ((24, 48), (16, 40), (20, 48)):
+            with pytest.raises(ValueError, match="16-byte aligned"):
+                thff.ThunderFFT_global(T, 64, True, x, y, 1)
+        with pytest.raises(ValueError, match="16-byte aligned"):
+            thff.ThunderFFT_conv1d(T, 64, 16, 24, 48, 1)
+        with pytest.raises(ValueError, match="16-byte aligned"):
+            thff.ThunderFFT_conv1d(T, 64, 16, 32, 56, 1, False)
+        with pytest.raises(ValueError, match="16-byte aligned"):
+            thff.ThunderFFT_conv2d(T, 64, 64, 24, 32, 48, 1)

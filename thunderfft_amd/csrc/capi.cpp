@@ -148,6 +148,10 @@ int cached_table(int precision, int n, const char* who, const float2** table, in
                               std::to_string(n) + ") first");
 }
 
+// The kernels move 16-byte vectors: every buffer must start on a 16-byte
+// boundary (any hipMalloc'd pointer, and any offset of whole transforms).
+bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15) == 0; }
+
 int conv1d_impl(int precision, int n, const void* x, const void* h, void* y, int batch,
                 int per_signal_filter, void* stream, bool synchronize) {
     if (!supported_precision(precision))
@@ -159,6 +163,8 @@ int conv1d_impl(int precision, int n, const void* x, const void* h, void* y, int
         return fail(THFF_EINVAL, "ThunderFFT_conv1d requires non-null signal, filter and output");
     if (y == x || y == h)
         return fail(THFF_EINVAL, "ThunderFFT_conv1d output must not alias its inputs");
+    if (!aligned16(x) || !aligned16(h) || !aligned16(y))
+        return fail(THFF_EINVAL, "ThunderFFT_conv1d requires 16-byte aligned buffers");
     const long long fpb = thff::c2c_transforms_per_block(n);
     if ((static_cast<long long>(batch) + fpb - 1) / fpb * 256 > static_cast<long long>(UINT32_MAX))
         return fail(THFF_EINVAL, "ThunderFFT batch exceeds one launch for this length");
@@ -217,7 +223,7 @@ int conv1d_real_impl(int precision, int n, const void* x, const void* spectrum, 
         return fail(THFF_EINVAL, "ThunderFFT_conv1d_real requires non-null signal, spectrum and output");
     if (y == x || y == spectrum)
         return fail(THFF_EINVAL, "ThunderFFT_conv1d_real output must not alias its inputs");
-    if ((reinterpret_cast<std::uintptr_t>(x) | reinterpret_cast<std::uintptr_t>(y)) & 15)
+    if (!aligned16(x) || !aligned16(y))
         return fail(THFF_EINVAL, "ThunderFFT_conv1d_real requires 16-byte aligned signal and output");
     // Complex transforms: one per pair of signals of a channel.
     const long long transforms = (static_cast<long long>(batch) + 1) / 2 * channels;
@@ -282,6 +288,8 @@ int conv2d_impl(int precision, int rows, int cols, const void* x, const void* h,
         return fail(THFF_EINVAL, "ThunderFFT_conv2d requires non-null images, filter and output");
     if (y == x || y == h)
         return fail(THFF_EINVAL, "ThunderFFT_conv2d output must not alias its inputs");
+    if (!aligned16(x) || !aligned16(h) || !aligned16(y))
+        return fail(THFF_EINVAL, "ThunderFFT_conv2d requires 16-byte aligned buffers");
     if (batch > (1 << 24)) return fail(THFF_EINVAL, "ThunderFFT batch exceeds one launch");
     const float2* table = nullptr;
     int cus = 0;
@@ -306,6 +314,8 @@ int global_impl(int precision, int n, int forward, const void* d_input, void* d_
     if (batch == 0) return THFF_OK;
     if (!d_input || !d_output || d_input == d_output)
         return fail(THFF_EINVAL, "ThunderFFT requires separate non-null input/output buffers");
+    if (!aligned16(d_input) || !aligned16(d_output))
+        return fail(THFF_EINVAL, "ThunderFFT requires 16-byte aligned input/output buffers");
     // The dispatch grid counts work-items in 32 bits.
     const long long fpb = thff::c2c_transforms_per_block(n);
     const long long items = (static_cast<long long>(batch) + fpb - 1) / fpb * 256;
