@@ -41,6 +41,7 @@
 #pragma once
 
 #include "fft_core.hpp"
+#include "fft_tile.hpp"
 
 namespace thff {
 
