@@ -27,7 +27,7 @@ template <int N>
 constexpr LaunchShape launch_shape(int precision) {
     if (precision == 0) return N == 2048 ? LaunchShape{2, true} : LaunchShape{1, false};
     if (N <= 128) return {1, false};
-    if (N == 2048) return {4, true};  // N = 256 ... 4096 run MFMA kernels
+    if (N == 2048) return {2, true};  // N = 256 ... 4096 run MFMA kernels
     if (N == 4096) return {0, false};  // the three-stage kernel: grid sized to the device
     return {2, N == 1024};
 }
