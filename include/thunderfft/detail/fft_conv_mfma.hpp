@@ -460,3 +460,166 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
 }
 
 }  // namespace thff
+
+namespace thff {
+
+// Complex fused convolution at N = 4096 on the three-stage MFMA transform
+// (conv1d_kernel's contract, half2 storage): per tile (one signal) the
+// filter's forward transform (per-signal filters; a shared filter is
+// transformed once per workgroup), the signal's, the product with the
+// filter spectrum kept packed as half2 (1/N folded in) and the inverse from
+// registers, as in conv1d_real_mfma4096_kernel.  Grid: sized to the device
+// (a few workgroups per CU), the signals shared out evenly (grid_tiles).
+template <int N, bool kPerSignal>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
+                       __half2* __restrict__ y, int batch, const float2* __restrict__ tw) {
+    using P = Mfma4096;
+    static_assert(N == P::N, "the three-stage transform is N = 4096");
+    __shared__ __align__(16) unsigned xbuf[P::kExchange];
+    __shared__ __align__(16) unsigned obuf[P::kOut];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int n = lane & 15, q = lane >> 4;
+    unsigned* const region = xbuf + 4 * P::kMatrix * wave;
+    constexpr float kScale = 1.0f / N;
+
+    f16x8 a[2], ai[2], ai_regs[2];
+    dft16_operands<true>(a, lane);
+    dft16_operands<false>(ai, lane);
+    dft16_operands<false, true>(ai_regs, lane);
+    cpx w1f[4][4], w1i[4][4], w2[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float2 f = tw[((64 * wave + 4 * n + b) * (q + 4 * r)) & (N - 1)];
+            const float2 g = tw[((4 * wave + b + 16 * n) * (q + 4 * r)) & (N - 1)];
+            w1f[b][r] = cpx{f.x, -f.y};
+            w1i[b][r] = cpx{g.x, g.y};
+        }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float2 g = tw[(16 * n * (q + 4 * r)) & (N - 1)];
+        w2[r] = cpx{g.x, g.y};
+    }
+
+    auto stages23 = [&](cpx (&v)[4][4], const f16x8 (&op)[2], bool conj_w2) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const u32x4 raw = *reinterpret_cast<const u32x4*>(
+                region + P::kMatrix * b + 16 * n + 4 * ((q + (n >> 2)) & 3));
+            u32x4 xv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[e] = raw[(e + b) & 3];
+            dft16_block(op, as_f16x8(xv), v[b]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[b][r] = conj_w2 ? cmulc(v[b][r], w2[r]) : cmul(v[b][r], w2[r]);
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                region[(16 * b + q + 4 * r) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] =
+                    pack_half2(v[b][r]);
+        wave_lds_sync();
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const u32x4 xv = *reinterpret_cast<const u32x4*>(
+                region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+            dft16_block(op, as_f16x8(xv), v[b]);
+        }
+    };
+    // Forward transform of the 4096 values at src (callers: every wave done
+    // with xbuf before, as the first barrier inside requires).
+    auto forward = [&](const __half2* src, cpx (&v)[4][4]) {
+        u32x4 z[4];
+        const __half2* s = src + 64 * wave + 4 * n + 1024 * q;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) z[e] = ld_nt(reinterpret_cast<const u32x4*>(s + 256 * e));
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            u32x4 xv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[e] = z[e][b];
+            dft16_block(a, as_f16x8(xv), v[b]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], w1f[b][r]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                xbuf[xaddr4096(q + 4 * r, 4 * (n & 3) + b, 4 * wave + (n >> 2))] = pack_half2(v[b][r]);
+        __syncthreads();
+        stages23(v, a, true);
+    };
+
+    unsigned hp[4][4];  // FFT(h) / N at bins 4 w + b + 16 n + 256 (q + 4 r), packed half2
+    auto keep = [&](const cpx (&v)[4][4]) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) hp[b][r] = pack_half2({v[b][r].re * kScale, v[b][r].im * kScale});
+    };
+    long long tile, tile_end;
+    grid_tiles(batch, tile, tile_end);
+    if (tile >= tile_end) return;  // uniform over the workgroup
+    if constexpr (!kPerSignal) {
+        cpx v[4][4];
+        forward(h, v);
+        keep(v);
+    }
+    for (; tile < tile_end; ++tile) {
+        cpx v[4][4];
+        if constexpr (kPerSignal) {
+            forward(h + tile * N, v);
+            keep(v);
+        }
+        forward(x + tile * N, v);
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float2 hk = __half22float2(__builtin_bit_cast(__half2, hp[b][r]));
+                v[b][r] = cmul(v[b][r], cpx{hk.x, hk.y});
+            }
+        // ---- inverse: stage 1 from the registers, exchange, stages 2-3 ----
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            u32x4 xv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) xv[r] = pack_half2(v[b][r]);
+            dft16_block(ai_regs, as_f16x8(xv), v[b]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], w1i[b][r]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                xbuf[xaddr4096(q + 4 * r, 4 * wave + b, n)] = pack_half2(v[b][r]);
+        __syncthreads();
+        stages23(v, ai, false);
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                obuf[P::out_pad(4 * wave + b + 16 * n + 256 * (q + 4 * r))] = pack_half2(v[b][r]);
+        __syncthreads();
+        __half2* dst = y + tile * N;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * tid + 1024 * i;
+            u32x4 o;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o[c] = obuf[P::out_pad(e + c)];
+            st_nt(reinterpret_cast<u32x4*>(dst + e), o);
+        }
+    }
+}
+
+}  // namespace thff

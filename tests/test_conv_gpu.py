@@ -124,6 +124,60 @@ def test_config4_conv1d_2048(T):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("per_signal", [True, False])
+def test_conv1d_4096_many_signals_per_workgroup(T, per_signal):
+    """2112 signals of 4096: more signals than workgroups, so every workgroup
+    convolves several in turn (a shared filter is transformed once per
+    workgroup).  A subset against the direct convolution, then every signal
+    through the impulse roll (per-signal shifts, or one shared shift)."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    n, batch = 4096, 2112
+    dt = torch.float32 if T == "float" else torch.float16
+    seed = oracle.BENCH_SEED_BASE + n + 11
+    x = torch.empty(2 * n * batch, dtype=dt, device="cuda")
+    thff.fill_uniform(T, x, n * batch, seed)
+    y = torch.full_like(x, float("nan"))
+    thff.ThunderFFTInitialize(T, n)
+    nh = batch if per_signal else 1
+    mode = "per-signal" if per_signal else "shared"
+
+    rows = np.unique(np.concatenate([np.linspace(0, batch - 1, 12).astype(np.int64),
+                                     np.arange(batch - 2, batch)]))
+    h_host = oracle.represent(_filters(n, nh, seed=41).reshape(nh, n), T)
+    thff.ThunderFFT_conv1d(T, n, x, to_device(h_host, T), y, batch, per_signal)
+    rows_t = torch.from_numpy(rows).cuda()
+    sub = from_device(y.view(batch, 2 * n).index_select(0, rows_t).contiguous(), T)
+    sub = sub.reshape(len(rows), n)
+    xin = np.concatenate([oracle.uniform(n, 1, seed, first_element=int(r) * n) for r in rows])
+    ref = oracle.circconv1d(oracle.represent(xin, T),
+                            h_host[rows] if per_signal else h_host, per_signal)
+    m = oracle.metrics(sub, ref)
+    print(f"{T} conv1d N={n} batch={batch} {mode} subset rel_l2={m['rel_l2']:.3e}", flush=True)
+    assert m["nonfinite"] == 0 and m["rel_l2"] <= GATE and m["rel_l2"] <= TIGHT[T]
+
+    shifts = (13 * np.arange(nh) + 5) % n
+    imp = torch.zeros(nh, n, 2, dtype=dt, device="cuda")
+    imp[torch.arange(nh, device="cuda"), torch.from_numpy(shifts).cuda(), 0] = 1
+    y.fill_(float("nan"))
+    thff.ThunderFFT_conv1d(T, n, x, imp, y, batch, per_signal)
+    xs = x.view(batch, n, 2).float()
+    s = torch.from_numpy(np.broadcast_to(shifts, (batch,)).copy()).cuda()
+    idx = (torch.arange(n, device="cuda")[None, :] - s[:, None]) % n
+    want = torch.gather(xs, 1, idx[:, :, None].expand(batch, n, 2))
+    got = y.view(batch, n, 2).float()
+    assert bool(torch.isfinite(got).all())
+    err = float(torch.linalg.vector_norm(got - want) / torch.linalg.vector_norm(want))
+    worst = float((got - want).abs().max())
+    print(f"  impulse roll over all signals rel_l2={err:.3e} max={worst:.3e}", flush=True)
+    assert err <= TIGHT[T] and worst <= (5e-3 if T == "half" else 1e-5)
+    del x, y, imp
+    torch.cuda.empty_cache()
+
+
 def _filter2d(seed, full=False):
     """BASELINE config 5 filter: real 64 x 64, nonzero 7 x 7 corner block with
     i.i.d. N(0, 1/7) taps (full=True: every tap nonzero, complex)."""

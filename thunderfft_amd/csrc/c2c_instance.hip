@@ -144,6 +144,26 @@ hipError_t launch_conv1d(int precision, bool per_signal_filter, const void* x, c
             return hipGetLastError();
         }
     }
+    // fp16 N = 4096: the three-stage MFMA transform, one signal per tile, the
+    // grid sized to the kernel's occupancy (per-signal filters: 167 VGPRs, 3
+    // workgroups per CU; a shared filter keeps its spectrum live across the
+    // loop: 229 VGPRs, 2 per CU) with the signals shared out evenly.  2^25
+    // values on MI355X: 109 vs 162 us per-signal, 76 vs 125 us shared,
+    // against the VALU path.
+    if constexpr (N == 4096) {
+        if (precision != 0) {
+            const long long cap = (per_signal_filter ? 3LL : 2LL) * (num_cus > 0 ? num_cus : 256);
+            const unsigned grid = static_cast<unsigned>(batch < cap ? batch : cap);
+            const auto* xx = static_cast<const __half2*>(x);
+            const auto* hh = static_cast<const __half2*>(h);
+            auto* yy = static_cast<__half2*>(y);
+            if (per_signal_filter)
+                conv1d_mfma4096_kernel<N, true><<<grid, 256, 0, stream>>>(xx, hh, yy, batch, tw);
+            else
+                conv1d_mfma4096_kernel<N, false><<<grid, 256, 0, stream>>>(xx, hh, yy, batch, tw);
+            return hipGetLastError();
+        }
+    }
     using P = C2CPlan<N>;
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
     const int tpb = ntiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? 2 : 1;
