@@ -18,7 +18,8 @@ roofline.achieved = algorithmic bytes per launch (read + write of every
 complex value once: 2 * batch * N * sizeof(T)) / the mean launch duration
 above; roofline.traffic = HBM bytes per launch from the rocprofv3 FETCH_SIZE /
 WRITE_SIZE runs summarised in profiles/ (each scaled by what the counter reads
-for a plain copy of known size).  cpu_baseline = the oracle's threaded fp32
+for a plain copy of known size); also.*.mfma_util_pct = rocprofiler's MfmaUtil
+for the MFMA kernels, from the rocprofv3 run summarised there too.  cpu_baseline = the oracle's threaded fp32
 four-step (the reference has no CPU FFT) timed on this host's cores on a
 bounded sample of the same workload.
 """
@@ -37,6 +38,7 @@ N_FFT = 1024
 BATCH = 65536
 ROOT = os.path.dirname(os.path.abspath(__file__))
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "pmc_c2c_n1024_b65536.md")
+MFMA_PROFILE = os.path.join(ROOT, "profiles", "pmc_mfma_c2c_n1024_b65536.md")
 
 
 def parse():
@@ -361,15 +363,29 @@ def cpu_baseline(target_s: float) -> dict:
             "us_per_transform": dt * 1e6 / sample}
 
 
-def load_traffic(key: str):
-    """HBM bytes per launch for `key` (e.g. float_fwd) from the PMC summary."""
+def _profile_value(path: str, field: str, key: str):
+    """The value of the machine-readable line `field key: value` of a profile
+    summary, or None."""
     try:
-        with open(TRAFFIC_PROFILE) as f:
+        with open(path) as f:
             text = f.read()
     except OSError:
         return None
-    m = re.search(rf"^hbm_bytes_per_launch {re.escape(key)}: (\d+)\s*$", text, re.M)
-    return int(m.group(1)) if m else None
+    m = re.search(rf"^{field} {re.escape(key)}: ([0-9.]+)\s*$", text, re.M)
+    return m.group(1) if m else None
+
+
+def load_traffic(key: str):
+    """HBM bytes per launch for `key` (e.g. float_fwd) from the PMC summary."""
+    v = _profile_value(TRAFFIC_PROFILE, "hbm_bytes_per_launch", key)
+    return int(v) if v is not None else None
+
+
+def load_mfma_util(key: str):
+    """rocprofiler's MfmaUtil (% of SIMD cycles with the matrix cores busy)
+    for `key` (e.g. half_fwd) from the PMC summary."""
+    v = _profile_value(MFMA_PROFILE, "mfma_util_pct", key)
+    return float(v) if v is not None else None
 
 
 def prewarm(ms: float) -> float:
@@ -507,6 +523,9 @@ def main():
     }
     for k in out["also"]:
         out["also"][k]["hbm_traffic_bytes"] = load_traffic(k)
+        util = load_mfma_util(k)
+        if util is not None:
+            out["also"][k]["mfma_util_pct"] = util
     out["also"]["conv_note"] = ("conv1d bytes = x, h and y (3 * 2^25 complex); conv2d bytes = x "
                                 "and y (2 * 2^25 complex; the 32 KiB filter is read per "
                                 "workgroup from L2); conv1d_real bytes = x and y (2 * 2^26 "
