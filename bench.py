@@ -2,17 +2,20 @@
 """Benchmark of the hot path: batched C2C FFT, N=1024, batch 65536.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--cpu-seconds S]
-                    [--prewarm-ms M] [--sweep]
+                    [--prewarm-ms M] [--settle-ms S] [--sweep]
 
 One step = one ThunderFFT_global launch (the C ABI's asynchronous entry,
 thff_global_async) over the whole batch of 65536 signals of N=1024, inputs
 resident in HBM (generated on the device by thff_fill_uniform).  Before the
 first leg, M ms (default 250) of untimed launches bring the device to the
-clocks later legs see (prewarm_s in the output).  After W untimed steps, K
-steps run back to back between two HIP events recorded on the launch stream,
-bracketed by device synchronisation; ms_per_step is the event time / K.  value = GFLOP/s (5 N log2 N per transform) of the float
-forward transform; the inverse and the half transforms are measured the same
-way and reported under "also".
+clocks later legs see (prewarm_s in the output).  Per leg: W untimed steps,
+then untimed steps filling about S ms (default 60; settle_ms in the output,
+so that a heavy kernel is timed at its steady clocks rather than the
+transient after a pause), then K steps back to back between two HIP events
+recorded on the launch stream, bracketed by device synchronisation;
+ms_per_step is the event time / K.  value = GFLOP/s (5 N log2 N per
+transform) of the float forward transform; the inverse and the half
+transforms are measured the same way and reported under "also".
 
 roofline.achieved = algorithmic bytes per launch (read + write of every
 complex value once: 2 * batch * N * sizeof(T)) / the mean launch duration
@@ -52,10 +55,50 @@ def parse():
     ap.add_argument("--prewarm-ms", type=float, default=250.0,
                     help="untimed device warm-up before the first timed leg (ms of back-to-back "
                          "launches of that leg's kernel)")
+    ap.add_argument("--settle-ms", type=float, default=60.0,
+                    help="per leg, after its W warm-up launches: further untimed launches of "
+                         "that leg's kernel filling about this many ms before the timed ones")
     ap.add_argument("--sweep", action="store_true",
                     help="BASELINE config 3 instead: every N at batch 2^26/N, both types and "
                          "directions; prints one line per case and a JSON summary")
     return ap.parse_args()
+
+
+SETTLE_MS = 60.0  # set from --settle-ms in main()
+
+
+def timed(launch, steps: int, warmup: int, stream) -> float:
+    """Mean ms per launch of `launch` over `steps` back-to-back launches on
+    `stream`, timed with HIP events bracketed by device synchronisation.
+    Before them: `warmup` untimed launches, then as many more as fill about
+    SETTLE_MS (counted from the warm-up's own mean).  A heavy kernel started
+    after a pause first runs at transient clocks on MI355X: the fp32 conv1d
+    of 16384 x 2048 reads 165 us for ~12 launches, 220-230 us for the next
+    ~20, then climbs back over ~200 launches (~35 ms) to a steady 163-167 us.
+    Settling times that steady state."""
+    import torch
+
+    w0 = torch.cuda.Event(enable_timing=True)
+    w1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    w0.record(stream)
+    for _ in range(warmup):
+        launch()
+    w1.record(stream)
+    torch.cuda.synchronize()
+    if SETTLE_MS > 0 and warmup > 0:
+        per_ms = max(w0.elapsed_time(w1) / warmup, 1e-3)
+        for _ in range(int(math.ceil(SETTLE_MS / per_ms))):
+            launch()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(steps):
+        launch()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
 
 
 def time_gpu(T: str, forward: bool, steps: int, warmup: int, n: int = N_FFT,
@@ -71,19 +114,10 @@ def time_gpu(T: str, forward: bool, steps: int, warmup: int, n: int = N_FFT,
     stream = torch.cuda.current_stream()
     thff.fill_uniform(T, x, n * batch, 0x7F4A7C15 + n, 0, stream)
     thff.ThunderFFTInitialize(T, n)
-    for _ in range(warmup):
-        thff.ThunderFFT_global_async(T, n, forward, x, y, batch, stream)
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(steps):
-        thff.ThunderFFT_global_async(T, n, forward, x, y, batch, stream)
-    end.record(stream)
-    torch.cuda.synchronize()
+    ms = timed(lambda: thff.ThunderFFT_global_async(T, n, forward, x, y, batch, stream),
+               steps, warmup, stream)
     wall = time.perf_counter() - t0
-    ms = start.elapsed_time(end) / steps
     nbytes = 2 * n * batch * elem
     flops = 5.0 * n * math.log2(n) * batch
     del x, y
@@ -137,17 +171,7 @@ def time_conv(kind: str, T: str, steps: int, warmup: int) -> dict:
         else:
             thff.ThunderFFT_conv2d_async(T, 64, 64, x, h, y, batch, stream)
 
-    for _ in range(warmup):
-        launch()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
-    for _ in range(steps):
-        launch()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    ms = timed(launch, steps, warmup, stream)
     thff.ThunderFFTFinalize(T)
     del x, y, h
     return {"workload": (f"{kind} {batch} x {'2048' if kind == 'conv1d' else '64x64'} "
@@ -186,17 +210,7 @@ def time_conv_real(T: str, n: int, steps: int, warmup: int) -> dict:
     def launch():
         thff.ThunderFFT_conv1d_real_async(T, n, x, spectrum, y, batch, channels, stream)
 
-    for _ in range(warmup):
-        launch()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
-    for _ in range(steps):
-        launch()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    ms = timed(launch, steps, warmup, stream)
     thff.ThunderFFTFinalize(T)
     nbytes = 2 * count * elem  # x and y; the spectra (2 MiB) stay in L2
     transforms = count // (2 * n)  # two real signals per complex transform
@@ -232,17 +246,7 @@ def time_conv_valid(T: str, ntaps: int, steps: int, warmup: int) -> dict:
     def launch():
         thff.ThunderFFT_conv1d_valid_async(T, x, length, taps, ntaps, y, 1, stream)
 
-    for _ in range(warmup):
-        launch()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
-    for _ in range(steps):
-        launch()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    ms = timed(launch, steps, warmup, stream)
     thff.ThunderFFTFinalize(T)
     nbytes = (length + out_len) * elem
     windows = -(-out_len // (65 - ntaps))
@@ -431,7 +435,8 @@ def sweep(a) -> None:
                       f"({r['pct_hbm_peak']:.1f}% of HBM peak), {r['gflops']:.0f} GFLOP/s",
                       file=sys.stderr, flush=True)
             thff.ThunderFFTFinalize(T)
-    print(json.dumps({"sweep": out, "steps": a.steps, "warmup": a.warmup}), flush=True)
+    print(json.dumps({"sweep": out, "steps": a.steps, "warmup": a.warmup,
+                      "settle_ms": a.settle_ms}), flush=True)
 
 
 def main():
@@ -450,6 +455,8 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
     thff.lib()
+    global SETTLE_MS
+    SETTLE_MS = a.settle_ms
     prewarm_s = prewarm(a.prewarm_ms)
     if a.sweep:
         sweep(a)
@@ -499,6 +506,7 @@ def main():
         "steps": a.steps,
         "warmup": a.warmup,
         "prewarm_s": round(prewarm_s, 3),
+        "settle_ms": a.settle_ms,
         "ms_per_step": round(main_run["us_per_call"] / 1e3, 6),
         "higher_is_better": True,
         "scaling": "weak",

@@ -6,8 +6,8 @@
 // fewer than kFPB valid transforms, whose inputs are never read (they are
 // zero-filled) and whose outputs are never written.
 //
-// A workgroup walks `tiles_per_block` consecutive tiles of 4096 values
-// (fft_tile.hpp).  Each wave reads its quarter of a tile with 16-byte
+// A workgroup walks `tiles_per_block` consecutive tiles of 4096 values, or
+// with 0 every G-th tile of a device-sized grid (tile_walk, fft_tile.hpp).  Each wave reads its quarter of a tile with 16-byte
 // non-temporal loads and redistributes it through LDS into the first pass's
 // layout; the output leaves the same way, so all global traffic is fully
 // coalesced dwordx4.  kPrefetch keeps the next tile's loads in flight while
@@ -38,17 +38,17 @@ c2c_kernel(const IO* __restrict__ in, IO* __restrict__ out, int batch, const flo
     w.load(io.t, tw);
 
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
-    long long tile, tile_end;
-    block_tiles(ntiles, tiles_per_block, tile, tile_end);
+    long long tile, tile_end, step;
+    tile_walk(ntiles, tiles_per_block, tile, tile_end, step);
     if (tile >= tile_end) return;  // uniform over the workgroup
 
     typename T::Raw next;
     if constexpr (kPrefetch) io.load(next, in, tile, batch);
-    for (; tile < tile_end; ++tile) {
+    for (; tile < tile_end; tile += step) {
         typename T::Raw cur;
         if constexpr (kPrefetch) {
             cur = next;
-            if (tile + 1 < tile_end) io.load(next, in, tile + 1, batch);
+            if (tile + step < tile_end) io.load(next, in, tile + step, batch);
         } else {
             io.load(cur, in, tile, batch);
         }

@@ -39,8 +39,8 @@ conv1d_kernel(const IO* __restrict__ x, const IO* __restrict__ h, IO* __restrict
     constexpr float kScale = 1.0f / N;
 
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
-    long long tile, tile_end;
-    block_tiles(ntiles, tiles_per_block, tile, tile_end);
+    long long tile, tile_end, step;
+    tile_walk(ntiles, tiles_per_block, tile, tile_end, step);
     if (tile >= tile_end) return;  // uniform over the workgroup
 
     cpx hs[16];  // this lane's share of the scaled filter spectrum, H[t + TPF*j] / N
@@ -54,7 +54,7 @@ conv1d_kernel(const IO* __restrict__ x, const IO* __restrict__ h, IO* __restrict
         for (int j = 0; j < 16; ++j) hs[j] = {hs[j].re * kScale, hs[j].im * kScale};
     }
 
-    for (; tile < tile_end; ++tile) {
+    for (; tile < tile_end; tile += step) {
         cpx v[16];
         if constexpr (kPerSignal) {
             // The filter first, so its raw tile is dead before the signal's
@@ -153,8 +153,8 @@ __global__ __launch_bounds__(256) void conv2d64_kernel(const IO* __restrict__ x,
     w.load(io.t, tw);
     constexpr float kScale = 1.0f / 4096.0f;
 
-    long long tile, tile_end;
-    block_tiles(batch, tiles_per_block, tile, tile_end);
+    long long tile, tile_end, step;
+    tile_walk(batch, tiles_per_block, tile, tile_end, step);
     if (tile >= tile_end) return;  // uniform over the workgroup
 
     cpx hs[16];  // FFT2(h) / 4096 in the transposed-spectrum layout
@@ -167,7 +167,7 @@ __global__ __launch_bounds__(256) void conv2d64_kernel(const IO* __restrict__ x,
         for (int j = 0; j < 16; ++j) hs[j] = {hs[j].re * kScale, hs[j].im * kScale};
     }
     const long long rows = 64LL * batch;  // TileIO counts 64-point row transforms
-    for (; tile < tile_end; ++tile) {
+    for (; tile < tile_end; tile += step) {
         typename T::Raw r;
         io.load(r, x, tile, rows);
         cpx v[16];
@@ -286,10 +286,10 @@ __global__ __launch_bounds__(256) void conv1d_real_kernel(
     const long long pairs = (static_cast<long long>(batch) + 1) / 2;
     const long long transforms = pairs * channels;
     const long long ntiles = (transforms + P::kFPB - 1) / P::kFPB;
-    long long tile, tile_end;
-    block_tiles(ntiles, tiles_per_block, tile, tile_end);
+    long long tile, tile_end, step;
+    tile_walk(ntiles, tiles_per_block, tile, tile_end, step);
 
-    for (; tile < tile_end; ++tile) {
+    for (; tile < tile_end; tile += step) {
         // ---- both rows of each transform -> LDS as (re, im) = (row 0, row 1) ----
         long long base0[kSteps], base1[kSteps];  // element offsets, -1 = no row
 #pragma unroll

@@ -74,13 +74,10 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
     const long long pairs = (static_cast<long long>(batch) + 1) / 2;
     const long long transforms = pairs * channels;
     const long long ntiles = (transforms + P::kFPB - 1) / P::kFPB;
-    long long tile, tile_end;  // tiles_per_block = 0: balanced shares of a device-sized grid
-    if (tiles_per_block > 0)
-        block_tiles(ntiles, tiles_per_block, tile, tile_end);
-    else
-        grid_tiles(ntiles, tile, tile_end);
+    long long tile, tile_end, step;
+    tile_walk(ntiles, tiles_per_block, tile, tile_end, step);
 
-    for (; tile < tile_end; ++tile) {
+    for (; tile < tile_end; tile += step) {
         // Rows of this wave's transforms, as element offsets (-1: none).
         long long base0[2], base1[2];
         int chan[P::kFPW];
@@ -190,11 +187,8 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
     dft16_operands<false, true>(ai_regs, lane);
 
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
-    long long tile, tile_end;  // tiles_per_block = 0: balanced shares of a device-sized grid
-    if (tiles_per_block > 0)
-        block_tiles(ntiles, tiles_per_block, tile, tile_end);
-    else
-        grid_tiles(ntiles, tile, tile_end);
+    long long tile, tile_end, step;
+    tile_walk(ntiles, tiles_per_block, tile, tile_end, step);
 
     // Valid values (0..kWaveVals) of this wave's transforms in tile tl.
     auto valid = [&](long long tl) {
@@ -241,7 +235,7 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
         keep(v);
     }
 
-    for (; tile < tile_end; ++tile) {
+    for (; tile < tile_end; tile += step) {
         const int nv = valid(tile);
         const long long off = (tile * P::kFPB + wave * P::kFPW) * N;
         cpx v[kB][4];
@@ -341,14 +335,11 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
         w2[r] = cpx{g.x, g.y};
     }
 
-    // tiles_per_block = 0: the grid is sized to the device and the transforms
-    // are shared out evenly (grid_tiles); otherwise contiguous runs.
+    // tiles_per_block = 0: the grid is sized to the device and walks the
+    // transforms grid-stride (tile_walk); otherwise contiguous runs.
     const long long transforms = (static_cast<long long>(batch) + 1) / 2 * channels;
-    long long tile, tile_end;
-    if (tiles_per_block > 0)
-        block_tiles(transforms, tiles_per_block, tile, tile_end);
-    else
-        grid_tiles(transforms, tile, tile_end);
+    long long tile, tile_end, step;
+    tile_walk(transforms, tiles_per_block, tile, tile_end, step);
 
     // Stage 2 of either direction, the wave-local transpose and stage 3.
     auto stages23 = [&](cpx (&v)[4][4], const f16x8 (&op)[2], bool conj_w2) {
@@ -379,7 +370,7 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
         }
     };
 
-    for (; tile < tile_end; ++tile) {
+    for (; tile < tile_end; tile += step) {
         const long long p = tile / channels, d = tile - p * channels;
         const long long row0 = (2 * p * channels + d) * N;
         const long long row1 = 2 * p + 1 < batch ? ((2 * p + 1) * channels + d) * N : -1;
@@ -469,9 +460,15 @@ namespace thff {
 // transformed once per workgroup), the signal's, the product with the
 // filter spectrum kept packed as half2 (1/N folded in) and the inverse from
 // registers, as in conv1d_real_mfma4096_kernel.  Grid: sized to the device
-// (a few workgroups per CU), the signals shared out evenly (grid_tiles).
+// (a few workgroups per CU), walking the signals grid-stride (tile_walk).
+// Per-signal filters: held to 168 VGPRs (3 workgroups per CU) at the cost of a
+// 32-byte spill, 103 us against 111 us at 2 per CU (2^25 values, MI355X).  A
+// shared filter keeps its spectrum live across the loop: 2 per CU.
+template <bool kPerSignal>
+inline constexpr int kConv4096MinWavesPerEU = kPerSignal ? 3 : 2;
+
 template <int N, bool kPerSignal>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kConv4096MinWavesPerEU<kPerSignal>))) void
 conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
                        __half2* __restrict__ y, int batch, const float2* __restrict__ tw) {
     using P = Mfma4096;
@@ -564,15 +561,15 @@ conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict_
 #pragma unroll
             for (int r = 0; r < 4; ++r) hp[b][r] = pack_half2({v[b][r].re * kScale, v[b][r].im * kScale});
     };
-    long long tile, tile_end;
-    grid_tiles(batch, tile, tile_end);
+    long long tile, tile_end, step;
+    tile_walk(batch, 0, tile, tile_end, step);
     if (tile >= tile_end) return;  // uniform over the workgroup
     if constexpr (!kPerSignal) {
         cpx v[4][4];
         forward(h, v);
         keep(v);
     }
-    for (; tile < tile_end; ++tile) {
+    for (; tile < tile_end; tile += step) {
         cpx v[4][4];
         if constexpr (kPerSignal) {
             forward(h + tile * N, v);

@@ -278,11 +278,8 @@ c2c_mfma_kernel(const __half2* __restrict__ in,
     mfma_setup<C, FWD>(a, w1, w2, tw);
 
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
-    long long tile, tile_end;  // tiles_per_block = 0: balanced shares of a device-sized grid
-    if (tiles_per_block > 0)
-        block_tiles(ntiles, tiles_per_block, tile, tile_end);
-    else
-        grid_tiles(ntiles, tile, tile_end);
+    long long tile, tile_end, step;
+    tile_walk(ntiles, tiles_per_block, tile, tile_end, step);
     if (tile >= tile_end) return;  // uniform over the workgroup
 
     // Valid values (0..kWaveVals) of this wave's kFPW transforms in tile tl.
@@ -302,12 +299,12 @@ c2c_mfma_kernel(const __half2* __restrict__ in,
 
     u32x4 next[kRaw];
     if constexpr (kPrefetch) load(next, tile);
-    for (; tile < tile_end; ++tile) {
+    for (; tile < tile_end; tile += step) {
         u32x4 cur[kRaw];
         if constexpr (kPrefetch) {
 #pragma unroll
             for (int i = 0; i < kRaw; ++i) cur[i] = next[i];
-            if (tile + 1 < tile_end) load(next, tile + 1);
+            if (tile + step < tile_end) load(next, tile + step);
         } else {
             load(cur, tile);
         }
@@ -406,13 +403,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
         w2[r] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
     }
 
-    // tiles_per_block = 0: the grid is sized to the device and the batch is
-    // shared out evenly (grid_tiles); otherwise contiguous runs of that many.
-    long long tile, tile_end;
-    if (tiles_per_block > 0)
-        block_tiles(batch, tiles_per_block, tile, tile_end);
-    else
-        grid_tiles(batch, tile, tile_end);
+    // tiles_per_block = 0: the grid is sized to the device and walks the batch
+    // grid-stride (tile_walk); otherwise contiguous runs of that many.
+    long long tile, tile_end, step;
+    tile_walk(batch, tiles_per_block, tile, tile_end, step);
     if (tile >= tile_end) return;  // uniform over the workgroup
 
     // Input j = 4 q + e of the lane's blocks b = 0..3: x[64 wave + 4 n + b + 256 j].
@@ -424,12 +418,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
 
     u32x4 next[4];
     if constexpr (kPrefetch) load(next, tile);
-    for (; tile < tile_end; ++tile) {
+    for (; tile < tile_end; tile += step) {
         u32x4 cur[4];
         if constexpr (kPrefetch) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) cur[i] = next[i];
-            if (tile + 1 < tile_end) load(next, tile + 1);
+            if (tile + step < tile_end) load(next, tile + step);
         } else {
             load(cur, tile);
         }

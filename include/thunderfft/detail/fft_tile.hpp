@@ -262,20 +262,25 @@ struct TileIO {
     }
 };
 
-// Tiles [first, end) of the workgroup; first >= end when it has none.
-__device__ __forceinline__ void block_tiles(long long ntiles, int tiles_per_block, long long& first,
-                                            long long& end) {
-    first = static_cast<long long>(blockIdx.x) * tiles_per_block;
-    end = first + tiles_per_block < ntiles ? first + tiles_per_block : ntiles;
-}
-
-// Balanced share of ntiles over the grid: [b T / G, (b + 1) T / G), so the
-// workgroups' tile counts differ by at most one (for grids sized to the
-// device rather than to the batch).
-__device__ __forceinline__ void grid_tiles(long long ntiles, long long& first, long long& end) {
-    const long long g = gridDim.x, b = blockIdx.x;
-    first = b * ntiles / g;
-    end = (b + 1) * ntiles / g;
+// The tiles of workgroup blockIdx.x: first, first + step, ... while < end
+// (first >= end when it has none).
+//   tiles_per_block > 0: a contiguous run of that many (grids sized to the batch).
+//   tiles_per_block = 0: grid-stride, tiles b, b + G, b + 2G, ... (grids sized to
+//     the device).  The workgroups resident at any moment then work on
+//     neighbouring tiles, so their traffic spreads over the HBM channels;
+//     contiguous per-workgroup shares put the concurrent accesses a share apart
+//     and measured 3-10% slower on MI355X.
+__device__ __forceinline__ void tile_walk(long long ntiles, int tiles_per_block, long long& first,
+                                          long long& end, long long& step) {
+    if (tiles_per_block > 0) {
+        first = static_cast<long long>(blockIdx.x) * tiles_per_block;
+        end = first + tiles_per_block < ntiles ? first + tiles_per_block : ntiles;
+        step = 1;
+    } else {
+        first = blockIdx.x;
+        end = ntiles;
+        step = gridDim.x;
+    }
 }
 
 }  // namespace thff

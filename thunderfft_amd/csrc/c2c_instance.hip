@@ -15,21 +15,44 @@
 
 namespace thff {
 
-// Launch shape per (N, precision), from sweeps on MI355X at batch = 2^26/N
-// with random inputs: tiles each workgroup walks, and whether the next
-// tile's loads are issued before the current tile is transformed.
+// Grids.  per_cu = 0: one workgroup per tile.  per_cu = k: min(ntiles, k x
+// CUs) workgroups walking the tiles grid-stride (tiles_per_block = 0,
+// tile_walk in fft_tile.hpp), so the workgroups resident at any moment work
+// on neighbouring tiles and one workgroup's set-up (twiddles, DFT operands, a
+// shared filter's transform) serves many tiles.  The k of each kernel below
+// is the fastest of 1, 2, 3, 4, 6, 8 and 16 on MI355X at 2^25-2^26 values
+// per array (usually the kernel's occupancy in workgroups per CU).
+struct Grid {
+    unsigned blocks;
+    int tiles_per_block;
+};
+
+inline Grid make_grid(long long ntiles, int per_cu, int num_cus) {
+    if (per_cu <= 0) return {static_cast<unsigned>(ntiles), 1};
+    const long long g = static_cast<long long>(per_cu) * (num_cus > 0 ? num_cus : 256);
+    return {static_cast<unsigned>(ntiles < g ? ntiles : g), 0};
+}
+
+// C2C launch shape per (N, precision): workgroups per CU (make_grid) and
+// whether the next tile's loads are issued before the current tile is
+// transformed.  Measured at batch = 2^26/N:
+//   fp32 N <= 1024: one tile per workgroup, 172-177 us (device grids: 181+).
+//   fp32 N = 2048, 4096: 16 per CU with prefetch, 184 us (one or two tiles
+//     per workgroup: 188-194 us).
+//   fp16 N = 64, 128 (VALU): one tile per workgroup.
+//   fp16 MFMA: 2 per CU, 87-94 us (two tiles per workgroup: 87-98 us; N = 4096
+//     with contiguous shares: 99 us); N = 2048 without prefetch, which would
+//     drop the kernel to one workgroup per CU.
 struct LaunchShape {
-    int tiles;
+    int per_cu;
     bool prefetch;
 };
 
 template <int N>
 constexpr LaunchShape launch_shape(int precision) {
-    if (precision == 0) return N == 2048 ? LaunchShape{2, true} : LaunchShape{1, false};
-    if (N <= 128) return {1, false};
-    if (N == 2048) return {2, true};  // N = 256 ... 4096 run MFMA kernels
-    if (N == 4096) return {0, false};  // the three-stage kernel: grid sized to the device
-    return {2, N == 1024};
+    if (precision == 0) return N <= 1024 ? LaunchShape{0, false} : LaunchShape{16, true};
+    if (N <= 128) return {0, false};
+    return {2, N != 2048};
 }
 
 // half2 lengths whose radix-16 stages run on MFMA (fft_mfma.hpp): N = 256*C
@@ -41,84 +64,87 @@ inline constexpr bool kHalfOnMfma3 = N == 4096;
 
 // Only the launch shape in use is instantiated.
 template <class IO, int N, bool FWD>
-void enqueue(unsigned grid, const IO* x, IO* y, int batch, const float2* tw, int tpb,
-             hipStream_t stream) {
+void enqueue(Grid g, const IO* x, IO* y, int batch, const float2* tw, hipStream_t stream) {
     constexpr bool kPf = launch_shape<N>(std::is_same_v<IO, float2> ? 0 : 1).prefetch;
-    c2c_kernel<IO, N, FWD, kPf><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
+    c2c_kernel<IO, N, FWD, kPf><<<g.blocks, 256, 0, stream>>>(x, y, batch, tw, g.tiles_per_block);
 }
 
 template <int N, bool FWD>
-void enqueue_mfma(unsigned grid, const __half2* x, __half2* y, int batch, const float2* tw,
-                  int tpb, hipStream_t stream) {
+void enqueue_mfma(Grid g, const __half2* x, __half2* y, int batch, const float2* tw,
+                  hipStream_t stream) {
     constexpr bool kPf = launch_shape<N>(1).prefetch;
-    c2c_mfma_kernel<N / 256, FWD, kPf><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
+    c2c_mfma_kernel<N / 256, FWD, kPf><<<g.blocks, 256, 0, stream>>>(x, y, batch, tw,
+                                                                     g.tiles_per_block);
 }
 
 template <bool FWD>
-void enqueue_mfma4096(unsigned grid, const __half2* x, __half2* y, int batch, const float2* tw,
-                      int tpb, hipStream_t stream) {
+void enqueue_mfma4096(Grid g, const __half2* x, __half2* y, int batch, const float2* tw,
+                      hipStream_t stream) {
     constexpr bool kPf = launch_shape<4096>(1).prefetch;
-    c2c_mfma4096_kernel<FWD, kPf><<<grid, 256, 0, stream>>>(x, y, batch, tw, tpb);
+    c2c_mfma4096_kernel<FWD, kPf><<<g.blocks, 256, 0, stream>>>(x, y, batch, tw,
+                                                                g.tiles_per_block);
 }
 
 template <int N>
 hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, int batch,
                       const float2* tw, int num_cus, hipStream_t stream) {
-    const LaunchShape shape = launch_shape<N>(precision);
     const bool mfma = precision != 0 && kHalfOnMfma<N>;
     long long fpb = C2CPlan<N>::kFPB;  // 1 for N = 4096 on either kernel
     if constexpr (kHalfOnMfma<N>)
         if (mfma) fpb = MfmaPlan<N / 256>::kFPB;
     const long long ntiles = (static_cast<long long>(batch) + fpb - 1) / fpb;
-    // Small batches spread one tile per workgroup over the whole device.
-    int tpb = ntiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? shape.tiles : 1;
-    unsigned grid = static_cast<unsigned>((ntiles + tpb - 1) / tpb);
-    if constexpr (kHalfOnMfma3<N>) {
-        // The three-stage kernel: 2 workgroups per CU sharing the batch evenly
-        // (tpb = 0) measured 99 us against 105-107 us for 4, 8 or 16 tiles per
-        // workgroup (2^26 values, MI355X); its set-up is the heaviest.
-        if (precision != 0) {
-            const long long cap = 2LL * (num_cus > 0 ? num_cus : 256);
-            grid = static_cast<unsigned>(ntiles < cap ? ntiles : cap);
-            tpb = 0;
-        }
-    }
+    const Grid g = make_grid(ntiles, launch_shape<N>(precision).per_cu, num_cus);
     if (precision == 0) {
         const auto* x = static_cast<const float2*>(in);
         auto* y = static_cast<float2*>(out);
         if (forward)
-            enqueue<float2, N, true>(grid, x, y, batch, tw, tpb, stream);
+            enqueue<float2, N, true>(g, x, y, batch, tw, stream);
         else
-            enqueue<float2, N, false>(grid, x, y, batch, tw, tpb, stream);
+            enqueue<float2, N, false>(g, x, y, batch, tw, stream);
     } else {
         const auto* x = static_cast<const __half2*>(in);
         auto* y = static_cast<__half2*>(out);
         if constexpr (kHalfOnMfma<N>) {
             if (forward)
-                enqueue_mfma<N, true>(grid, x, y, batch, tw, tpb, stream);
+                enqueue_mfma<N, true>(g, x, y, batch, tw, stream);
             else
-                enqueue_mfma<N, false>(grid, x, y, batch, tw, tpb, stream);
+                enqueue_mfma<N, false>(g, x, y, batch, tw, stream);
         } else if constexpr (kHalfOnMfma3<N>) {
             if (forward)
-                enqueue_mfma4096<true>(grid, x, y, batch, tw, tpb, stream);
+                enqueue_mfma4096<true>(g, x, y, batch, tw, stream);
             else
-                enqueue_mfma4096<false>(grid, x, y, batch, tw, tpb, stream);
+                enqueue_mfma4096<false>(g, x, y, batch, tw, stream);
         } else if (forward) {
-            enqueue<__half2, N, true>(grid, x, y, batch, tw, tpb, stream);
+            enqueue<__half2, N, true>(g, x, y, batch, tw, stream);
         } else {
-            enqueue<__half2, N, false>(grid, x, y, batch, tw, tpb, stream);
+            enqueue<__half2, N, false>(g, x, y, batch, tw, stream);
         }
     }
     return hipGetLastError();
 }
 
+// VALU convolution grids (conv1d_kernel, conv1d_real_kernel): fp32 up to
+// N = 1024 one tile per workgroup (127-175 us against 134-181 us for the best
+// device grid); otherwise the kernel's occupancy: N = 2048 3 per CU (fp32
+// conv1d 163 us against 172 us for two tiles per workgroup; fp16 real 111 vs
+// 121 us), N = 4096 2 per CU (174 vs 180 us; real 184 vs 195 us), fp16
+// N = 64, 128 4 per CU (real 64 vs 68 us) or 16 (conv1d 82-87 vs 85-91 us).
+template <int N>
+constexpr int valu_conv_per_cu(int precision, bool real) {
+    if (N >= 2048) return N == 2048 ? 3 : 2;
+    if (precision == 0) return 0;
+    return real ? 4 : 16;
+}
+
 template <class IO, int N>
-void enqueue_conv1d(bool per_signal, unsigned grid, const IO* x, const IO* h, IO* y, int batch,
-                    const float2* tw, int tpb, hipStream_t stream) {
+void enqueue_conv1d(bool per_signal, Grid g, const IO* x, const IO* h, IO* y, int batch,
+                    const float2* tw, hipStream_t stream) {
     if (per_signal)
-        conv1d_kernel<IO, N, true><<<grid, 256, 0, stream>>>(x, h, y, batch, tw, tpb);
+        conv1d_kernel<IO, N, true><<<g.blocks, 256, 0, stream>>>(x, h, y, batch, tw,
+                                                                 g.tiles_per_block);
     else
-        conv1d_kernel<IO, N, false><<<grid, 256, 0, stream>>>(x, h, y, batch, tw, tpb);
+        conv1d_kernel<IO, N, false><<<g.blocks, 256, 0, stream>>>(x, h, y, batch, tw,
+                                                                  g.tiles_per_block);
 }
 
 template <int N>
@@ -126,56 +152,57 @@ hipError_t launch_conv1d(int precision, bool per_signal_filter, const void* x, c
                          void* y, int batch, const float2* tw, int num_cus, hipStream_t stream) {
     // fp16 N = 256 ... 2048: all three transforms on MFMA (fft_conv_mfma.hpp);
     // per-signal filters, 2^25 values, against the VALU path on MI355X:
-    // 78 vs 90 us (N=256), 84 vs 116 (512), 93 vs 122 (1024), 106 vs 138 (2048).
+    // 77 vs 90 us (N=256), 83 vs 116 (512), 91 vs 122 (1024), 107 vs 138 (2048).
+    // Grid: the occupancy, 3 workgroups per CU (2 for N = 2048), 6% faster
+    // than 4 tiles per workgroup.
     if constexpr (N >= 256 && N <= 2048) {
         if (precision != 0) {
             constexpr int C = N / 256;
             using M = MfmaPlan<C>;
             const long long ntiles = (static_cast<long long>(batch) + M::kFPB - 1) / M::kFPB;
-            const int tpb = ntiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? (C == 8 ? 8 : 4) : 1;
-            const unsigned grid = static_cast<unsigned>((ntiles + tpb - 1) / tpb);
+            const Grid g = make_grid(ntiles, C == 8 ? 2 : 3, num_cus);
             const auto* xx = static_cast<const __half2*>(x);
             const auto* hh = static_cast<const __half2*>(h);
             auto* yy = static_cast<__half2*>(y);
             if (per_signal_filter)
-                conv1d_mfma_kernel<C, true><<<grid, 256, 0, stream>>>(xx, hh, yy, batch, tw, tpb);
+                conv1d_mfma_kernel<C, true><<<g.blocks, 256, 0, stream>>>(xx, hh, yy, batch, tw,
+                                                                          g.tiles_per_block);
             else
-                conv1d_mfma_kernel<C, false><<<grid, 256, 0, stream>>>(xx, hh, yy, batch, tw, tpb);
+                conv1d_mfma_kernel<C, false><<<g.blocks, 256, 0, stream>>>(xx, hh, yy, batch, tw,
+                                                                           g.tiles_per_block);
             return hipGetLastError();
         }
     }
     // fp16 N = 4096: the three-stage MFMA transform, one signal per tile, the
-    // grid sized to the kernel's occupancy (per-signal filters: 167 VGPRs, 3
-    // workgroups per CU; a shared filter keeps its spectrum live across the
-    // loop: 229 VGPRs, 2 per CU) with the signals shared out evenly.  2^25
-    // values on MI355X: 109 vs 162 us per-signal, 76 vs 125 us shared,
+    // grid at the kernel's occupancy (per-signal filters: 3 workgroups per CU;
+    // a shared filter keeps its spectrum live across the loop, 2 per CU).
+    // 2^25 values on MI355X: 103 vs 162 us per-signal, 76 vs 125 us shared,
     // against the VALU path.
     if constexpr (N == 4096) {
         if (precision != 0) {
-            const long long cap = (per_signal_filter ? 3LL : 2LL) * (num_cus > 0 ? num_cus : 256);
-            const unsigned grid = static_cast<unsigned>(batch < cap ? batch : cap);
+            const Grid g = make_grid(batch, per_signal_filter ? 3 : 2, num_cus);
             const auto* xx = static_cast<const __half2*>(x);
             const auto* hh = static_cast<const __half2*>(h);
             auto* yy = static_cast<__half2*>(y);
             if (per_signal_filter)
-                conv1d_mfma4096_kernel<N, true><<<grid, 256, 0, stream>>>(xx, hh, yy, batch, tw);
+                conv1d_mfma4096_kernel<N, true><<<g.blocks, 256, 0, stream>>>(xx, hh, yy, batch, tw);
             else
-                conv1d_mfma4096_kernel<N, false><<<grid, 256, 0, stream>>>(xx, hh, yy, batch, tw);
+                conv1d_mfma4096_kernel<N, false><<<g.blocks, 256, 0, stream>>>(xx, hh, yy, batch,
+                                                                               tw);
             return hipGetLastError();
         }
     }
     using P = C2CPlan<N>;
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
-    const int tpb = ntiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? 2 : 1;
-    const unsigned grid = static_cast<unsigned>((ntiles + tpb - 1) / tpb);
+    const Grid g = make_grid(ntiles, valu_conv_per_cu<N>(precision, false), num_cus);
     if (precision == 0)
-        enqueue_conv1d<float2, N>(per_signal_filter, grid, static_cast<const float2*>(x),
+        enqueue_conv1d<float2, N>(per_signal_filter, g, static_cast<const float2*>(x),
                                   static_cast<const float2*>(h), static_cast<float2*>(y), batch, tw,
-                                  tpb, stream);
+                                  stream);
     else
-        enqueue_conv1d<__half2, N>(per_signal_filter, grid, static_cast<const __half2*>(x),
+        enqueue_conv1d<__half2, N>(per_signal_filter, g, static_cast<const __half2*>(x),
                                    static_cast<const __half2*>(h), static_cast<__half2*>(y), batch,
-                                   tw, tpb, stream);
+                                   tw, stream);
     return hipGetLastError();
 }
 
@@ -195,46 +222,41 @@ hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectr
     using P = C2CPlan<N>;
     const long long transforms = (static_cast<long long>(batch) + 1) / 2 * channels;
     // fp16 N = 256 ... 1024: both transforms on MFMA (fft_conv_mfma.hpp);
-    // measured against this VALU path at 2^26 samples: 64 vs 68 us (N=256),
-    // 68 vs 87 (512), 74 vs 87 (1024).
+    // measured against this VALU path at 2^26 samples: 63 vs 68 us (N=256),
+    // 65 vs 87 (512), 70 vs 87 (1024).  Grid: the occupancy (3 workgroups per
+    // CU for N = 256, else 4), 9-11% faster than 4 tiles per workgroup.
     if constexpr (N >= 256 && N <= 1024) {
         if (precision != 0) {
-            // 4 tiles per workgroup amortise the set-up (twiddle table, three
-            // operand sets): 16-20% faster than 1 or 2 on MI355X.
             using M = MfmaPlan<N / 256>;
             const long long ntiles = (transforms + M::kFPB - 1) / M::kFPB;
-            const int tpb = ntiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? 4 : 1;
-            const unsigned grid = static_cast<unsigned>((ntiles + tpb - 1) / tpb);
-            conv1d_real_mfma_kernel<N / 256><<<grid, 256, 0, stream>>>(
+            const Grid g = make_grid(ntiles, N == 256 ? 3 : 4, num_cus);
+            conv1d_real_mfma_kernel<N / 256><<<g.blocks, 256, 0, stream>>>(
                 static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch, channels,
-                tw, tpb);
+                tw, g.tiles_per_block);
             return hipGetLastError();
         }
     }
-    // fp16 N = 4096: the three-stage MFMA transform, both directions.
+    // fp16 N = 4096: the three-stage MFMA transform, both directions; 2
+    // workgroups per CU: 86 us against 90-102 us for 3 or 4 (2^26 samples).
     if constexpr (N == 4096) {
         if (precision != 0) {
-            // 2 workgroups per CU sharing the transforms evenly: 87-90 us
-            // against 107 us for 4 tiles per workgroup (2^26 samples, MI355X).
-            const long long cap = 2LL * (num_cus > 0 ? num_cus : 256);
-            const unsigned grid = static_cast<unsigned>(transforms < cap ? transforms : cap);
-            conv1d_real_mfma4096_kernel<N><<<grid, 256, 0, stream>>>(
+            const Grid g = make_grid(transforms, 2, num_cus);
+            conv1d_real_mfma4096_kernel<N><<<g.blocks, 256, 0, stream>>>(
                 static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch, channels,
-                tw, 0);
+                tw, g.tiles_per_block);
             return hipGetLastError();
         }
     }
     const long long ntiles = (transforms + P::kFPB - 1) / P::kFPB;
-    const int tpb = ntiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? 2 : 1;
-    const unsigned grid = static_cast<unsigned>((ntiles + tpb - 1) / tpb);
+    const Grid g = make_grid(ntiles, valu_conv_per_cu<N>(precision, true), num_cus);
     if (precision == 0)
-        conv1d_real_kernel<float2, N><<<grid, 256, 0, stream>>>(
+        conv1d_real_kernel<float2, N><<<g.blocks, 256, 0, stream>>>(
             static_cast<const float*>(x), spectrum, static_cast<float*>(y), batch, channels, tw,
-            tpb);
+            g.tiles_per_block);
     else
-        conv1d_real_kernel<__half2, N><<<grid, 256, 0, stream>>>(
+        conv1d_real_kernel<__half2, N><<<g.blocks, 256, 0, stream>>>(
             static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch, channels, tw,
-            tpb);
+            g.tiles_per_block);
     return hipGetLastError();
 }
 
@@ -263,19 +285,18 @@ hipError_t launch_conv1d_valid(int precision, const void* x, long long len, cons
 
 hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y, int batch,
                            const float2* tw, int num_cus, hipStream_t stream) {
-    // One image per tile; a workgroup transforms the filter once, so it
-    // walks several images when the batch is large.
-    const long long tiles = batch;
-    const int tpb = tiles >= 16LL * (num_cus > 0 ? num_cus : 256) ? 8 : 1;
-    const unsigned grid = static_cast<unsigned>((tiles + tpb - 1) / tpb);
+    // One image per tile; each workgroup transforms the filter once.  4
+    // workgroups per CU (the occupancy): fp32 120 us, fp16 101 us for 8192
+    // images, against 127 / 104 us for 8 images per workgroup.
+    const Grid g = make_grid(batch, 4, num_cus);
     if (precision == 0)
-        conv2d64_kernel<float2><<<grid, 256, 0, stream>>>(static_cast<const float2*>(x),
-                                                          static_cast<const float2*>(h),
-                                                          static_cast<float2*>(y), batch, tw, tpb);
+        conv2d64_kernel<float2><<<g.blocks, 256, 0, stream>>>(
+            static_cast<const float2*>(x), static_cast<const float2*>(h), static_cast<float2*>(y),
+            batch, tw, g.tiles_per_block);
     else
-        conv2d64_kernel<__half2><<<grid, 256, 0, stream>>>(static_cast<const __half2*>(x),
-                                                           static_cast<const __half2*>(h),
-                                                           static_cast<__half2*>(y), batch, tw, tpb);
+        conv2d64_kernel<__half2><<<g.blocks, 256, 0, stream>>>(
+            static_cast<const __half2*>(x), static_cast<const __half2*>(h),
+            static_cast<__half2*>(y), batch, tw, g.tiles_per_block);
     return hipGetLastError();
 }
 #endif
