@@ -372,7 +372,9 @@ namespace thff {
 // writes the V valid outputs of each window back contiguously.  Nothing
 // crosses waves, so the kernel has no workgroup barrier after its set-up:
 // every workgroup transforms the filter once (fp32 taps) into a 64-value LDS
-// table G.
+// table G, then walks groups of 64 windows (one per transform slot) with
+// tile_walk: groups_per_block consecutive groups, or 0 for grid-stride over a
+// device-sized grid.
 // Inputs past the end of a signal read as zero; no valid output uses them.
 // Spans and output runs start at multiples of 16 values of their signal, so
 // signals that start on a 16-byte boundary move as whole 16-byte vectors
@@ -427,9 +429,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void c
         __syncthreads();
     }
 
-    long long g = static_cast<long long>(blockIdx.x) * groups_per_block;
-    const long long g_end = g + groups_per_block < groups ? g + groups_per_block : groups;
-    for (; g < g_end; ++g) {
+    long long g, g_end, step;
+    tile_walk(groups, groups_per_block, g, g_end, step);
+    for (; g < g_end; g += step) {
         const long long b = g / groups_per_signal;
         // This wave's first window, and where its input span and its outputs
         // start in signal b (both w0 * V, a multiple of 16 values).

@@ -265,21 +265,21 @@ hipError_t launch_conv1d_valid(int precision, const void* x, long long len, cons
                                int ntaps, void* y, int batch, const float2* tw, int num_cus,
                                hipStream_t stream) {
     // A group is the 64 windows (one per transform slot) of one workgroup
-    // pass; a workgroup walks several when there are many, so its filter
-    // transform is shared.
+    // pass; each workgroup transforms the filter once and walks many groups.
+    // 3 workgroups per CU (the occupancy): 2^26 values, 9 taps, 260 us fp32
+    // and 162 us fp16, against 294 / 174 us for runs of 4 groups.
     const long long valid = 65 - ntaps;
     const long long windows = (len - ntaps + 1 + valid - 1) / valid;
     const long long groups = (windows + 63) / 64 * batch;
-    const int gpb = groups >= 16LL * (num_cus > 0 ? num_cus : 256) ? 4 : 1;
-    const unsigned grid = static_cast<unsigned>((groups + gpb - 1) / gpb);
+    const Grid g = make_grid(groups, 3, num_cus);
     if (precision == 0)
-        conv1d_valid_kernel<float2><<<grid, 256, 0, stream>>>(
+        conv1d_valid_kernel<float2><<<g.blocks, 256, 0, stream>>>(
             static_cast<const float2*>(x), taps, static_cast<float2*>(y), len, ntaps, batch, tw,
-            gpb);
+            g.tiles_per_block);
     else
-        conv1d_valid_kernel<__half2><<<grid, 256, 0, stream>>>(
+        conv1d_valid_kernel<__half2><<<g.blocks, 256, 0, stream>>>(
             static_cast<const __half2*>(x), taps, static_cast<__half2*>(y), len, ntaps, batch, tw,
-            gpb);
+            g.tiles_per_block);
     return hipGetLastError();
 }
 
