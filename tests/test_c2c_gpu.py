@@ -220,6 +220,17 @@ def test_config3_sweep(T, n):
     _large_case(T, n, (1 << 26) // n)
 
 
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("n", SIZES)
+def test_grid_stride_walks(T, n):
+    """Batches of 514 full tiles and one partial tile: the kernels on
+    device-sized grids (2 workgroups per CU or more) hand some workgroups a
+    second tile a grid apart, and the partial tile is masked.  Forward only,
+    oracle on a subset of signals (first, last, spread) and the round trip."""
+    tile = 4096 // n  # transforms per 4096-value tile (every kernel)
+    _large_case(T, n, 514 * tile + max(1, tile // 2), directions=(True,))
+
+
 @pytest.mark.parametrize("mode", ["quick", "full"])
 def test_thff_validate_matrix(mode, tmp_path):
     """The thff_validate program (the reference's sample/validation/
