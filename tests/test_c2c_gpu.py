@@ -231,6 +231,46 @@ def test_grid_stride_walks(T, n):
     _large_case(T, n, 514 * tile + max(1, tile // 2), directions=(True,))
 
 
+@pytest.mark.parametrize("T,n", [("float", 1024), ("half", 1024), ("half", 4096), ("float", 4096)])
+def test_beyond_2e31_values(T, n):
+    """One launch over 2^31 + 5 * 4096 complex values (17 GB per fp32 buffer,
+    8.6 GB per fp16 buffer, on a 288 GB device): every signal offset past
+    2^31 values needs 64-bit index arithmetic.  Forward, the first signals,
+    the last ones and a spread between them against the oracle; then the
+    inverse of those signals back to N * x."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    batch = (1 << 31) // n + 5 * 4096 // n
+    count = n * batch
+    dt = torch.float32 if T == "float" else torch.float16
+    seed = oracle.BENCH_SEED_BASE + n + 31
+    x = torch.empty(2 * count, dtype=dt, device="cuda")
+    thff.fill_uniform(T, x, count, seed)
+    y = torch.empty_like(x)
+    thff.ThunderFFTInitialize(T, n)
+    thff.ThunderFFT_global(T, n, True, x, y, batch)
+    rows = np.unique(np.concatenate([np.arange(3), np.linspace(0, batch - 1, 24).astype(np.int64),
+                                     np.arange((1 << 31) // n - 2, batch)]))
+    rows_t = torch.from_numpy(rows).cuda()
+    sub = y.view(batch, 2 * n).index_select(0, rows_t).contiguous()
+    got = from_device(sub, T).reshape(len(rows), n)
+    xin = oracle.represent(np.concatenate([oracle.uniform(n, 1, seed, first_element=int(r) * n)
+                                           for r in rows]), T)
+    m = oracle.metrics(got, oracle.fft(xin, True))
+    print(f"{T} N={n} batch={batch} ({count} values) rows past 2^31: rel_l2={m['rel_l2']:.3e}",
+          flush=True)
+    assert m["nonfinite"] == 0 and m["rel_l2"] <= GATE and m["rel_l2"] <= TIGHT[T]
+    del x, y
+    back = torch.empty_like(sub)
+    thff.ThunderFFT_global(T, n, False, sub, back, len(rows))
+    rt = oracle.metrics(from_device(back, T).reshape(len(rows), n), n * xin.astype(np.complex128))
+    print(f"  round trip of the sampled signals rel_l2={rt['rel_l2']:.3e}", flush=True)
+    assert rt["nonfinite"] == 0 and rt["rel_l2"] <= 2 * TIGHT[T]
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("mode", ["quick", "full"])
 def test_thff_validate_matrix(mode, tmp_path):
     """The thff_validate program (the reference's sample/validation/

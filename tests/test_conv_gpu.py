@@ -178,6 +178,43 @@ def test_conv1d_4096_many_signals_per_workgroup(T, per_signal):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("T", ["half", "float"])
+def test_conv1d_beyond_2e31_values(T):
+    """Config 4's length over 2^31 + 3 * 2048 complex values per array (x, h and
+    y: 8.6 GB each in fp16, 17 GB in fp32): signal b's filter is a unit
+    impulse at (13 b + 5) mod N, so output row b is input row b rolled by that
+    shift; checked on the first rows, a spread and every row past value 2^31."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    n = 2048
+    batch = (1 << 31) // n + 3
+    dt = torch.float32 if T == "float" else torch.float16
+    x = torch.empty(2 * n * batch, dtype=dt, device="cuda")
+    thff.fill_uniform(T, x, n * batch, oracle.BENCH_SEED_BASE + 77)
+    shifts = (13 * torch.arange(batch, device="cuda") + 5) % n
+    h = torch.zeros(batch, n, 2, dtype=dt, device="cuda")
+    h[torch.arange(batch, device="cuda"), shifts, 0] = 1
+    y = torch.full_like(x, float("nan"))
+    thff.ThunderFFTInitialize(T, n)
+    thff.ThunderFFT_conv1d(T, n, x, h, y, batch, True)
+    del h
+    rows = torch.from_numpy(np.unique(np.concatenate([
+        np.arange(3), np.linspace(0, batch - 1, 16).astype(np.int64),
+        np.arange((1 << 31) // n - 2, batch)]))).cuda()
+    xs = x.view(batch, n, 2).index_select(0, rows).float()
+    ys = y.view(batch, n, 2).index_select(0, rows).float()
+    idx = (torch.arange(n, device="cuda")[None, :] - shifts[rows][:, None]) % n
+    want = torch.gather(xs, 1, idx[:, :, None].expand(len(rows), n, 2))
+    assert bool(torch.isfinite(ys).all())
+    err = float(torch.linalg.vector_norm(ys - want) / torch.linalg.vector_norm(want))
+    print(f"{T} conv1d N={n} batch={batch}: sampled rows rel_l2={err:.3e}", flush=True)
+    assert err <= TIGHT[T]
+    del x, y
+    torch.cuda.empty_cache()
+
+
 def _filter2d(seed, full=False):
     """BASELINE config 5 filter: real 64 x 64, nonzero 7 x 7 corner block with
     i.i.d. N(0, 1/7) taps (full=True: every tap nonzero, complex)."""
