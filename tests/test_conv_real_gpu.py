@@ -226,3 +226,47 @@ def test_full_size_impulse_rolls(T, n, batch, channels):
         # errors are spread evenly over a signal, so bound them against the
         # signal scale (|x| <= 1 here); a wrong shift or channel is O(1)
         assert rel <= 1e-3 and err.max() <= 5e-3, label
+
+
+@pytest.mark.parametrize("T", ["half", "float"])
+def test_beyond_2e31_samples(T):
+    """[8194][64][4096] real samples, 2^31 + 2^19 per array (4.3 GB fp16,
+    8.6 GB fp32), channel d's filter a unit impulse at (17 d + 1) mod N, so
+    every output row is its input row rolled; checked on the first rows, a
+    spread and every row past sample 2^31."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    n, channels = 4096, 64
+    batch = (1 << 31) // (channels * n) + 2
+    rows_total = batch * channels
+    shifts = (17 * np.arange(channels) + 1) % n
+    h = np.zeros((channels, n), dtype=np.float32)
+    h[np.arange(channels), shifts] = 1.0
+    thff.ThunderFFTInitialize(T, n)
+    d_x = torch.empty(rows_total * n, dtype=torch.float32 if T == "float" else torch.float16,
+                      device="cuda")
+    d_x.uniform_(-1, 1)
+    d_spec = spectra(T, n, h, 1.0 / n)
+    d_y = torch.full_like(d_x, float("nan"))
+    thff.ThunderFFT_conv1d_real(T, n, d_x, d_spec, d_y, batch, channels)
+    rows = torch.from_numpy(np.unique(np.concatenate([
+        np.arange(3), np.linspace(0, rows_total - 1, 16).astype(np.int64),
+        np.arange((1 << 31) // n - 2, rows_total)]))).cuda()
+    xs = d_x.view(rows_total, n).index_select(0, rows).float()
+    ys = d_y.view(rows_total, n).index_select(0, rows).float()
+    s = torch.from_numpy(shifts).cuda()[rows % channels]
+    idx = (torch.arange(n, device="cuda")[None, :] - s[:, None]) % n
+    want = torch.gather(xs, 1, idx)
+    assert bool(torch.isfinite(ys).all())
+    rel = float(torch.linalg.vector_norm(ys - want) / torch.linalg.vector_norm(want))
+    worst = float((ys - want).abs().max())
+    print(f"{T} real conv N={n} rows={rows_total}: sampled rows rel_l2={rel:.3e} "
+          f"max={worst:.3e}", flush=True)
+    if T == "float":
+        assert bool(((ys - want).abs() <= 1e-5 * want.abs() + 2e-6).all())
+    else:
+        assert rel <= 1e-3 and worst <= 5e-3
+    del d_x, d_y
+    torch.cuda.empty_cache()

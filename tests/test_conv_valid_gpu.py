@@ -139,3 +139,35 @@ def test_large_impulse_shifts(T, ntaps, k0):
     label = f"{T} F={ntaps} k0={k0}: max_err={err.max():.3e}"
     print(label, flush=True)
     assert np.all(np.isfinite(y)) and np.all(err <= tol), label
+
+
+@pytest.mark.parametrize("T", ["half", "float"])
+def test_signal_beyond_2e31_values(T):
+    """One signal of 2^31 + 777 complex values (8.6 GB fp16, 17 GB fp32) with a
+    unit impulse at tap 5 of 9: y[i] = x[i + 5].  Checked on the first 2^20
+    outputs and on every output from 2^31 - 2^20 to the end."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    ntaps, k0 = 9, 5
+    length = (1 << 31) + 777
+    out = length - ntaps + 1
+    dt = torch.float32 if T == "float" else torch.float16
+    d_x = torch.empty(2 * length, dtype=dt, device="cuda")
+    thff.fill_uniform(T, d_x, length, oracle.BENCH_SEED_BASE + 91)
+    f = np.zeros(ntaps, dtype=np.complex64)
+    f[k0] = 1.0
+    d_f = torch.from_numpy(f.view(np.float32)).cuda()
+    d_y = torch.full((2 * out,), float("nan"), dtype=dt, device="cuda")
+    thff.ThunderFFT_conv1d_valid(T, d_x, length, d_f, ntaps, d_y)
+    tol_rel = 1e-6 if T == "float" else 2.0 ** -10
+    for lo, hi in ((0, 1 << 20), ((1 << 31) - (1 << 20), out)):
+        y = d_y[2 * lo:2 * hi].float()
+        want = d_x[2 * (lo + k0):2 * (hi + k0)].float()
+        err = (y - want).abs()
+        ok = bool(torch.isfinite(y).all()) and bool((err <= tol_rel * want.abs() + 1e-6).all())
+        print(f"{T} outputs [{lo}, {hi}): max_err={float(err.max()):.3e}", flush=True)
+        assert ok, (T, lo, hi)
+    del d_x, d_y
+    torch.cuda.empty_cache()
