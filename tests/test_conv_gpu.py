@@ -283,3 +283,37 @@ def test_config5_conv2d_64x64():
     assert np.isfinite(err) and err <= TIGHT[T]
     del x, y
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+def test_conv2d_beyond_2e31_values(T):
+    """2^19 + 3 images of 64 x 64 (2^31 + 12288 complex values: 17 GB fp32,
+    8.6 GB fp16 per array) with a unit-impulse filter at (dr, dc): every image
+    rolls by (dr, dc); checked on the first images, a spread and every image
+    past value 2^31."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    batch = (1 << 19) + 3
+    dt = torch.float32 if T == "float" else torch.float16
+    x = torch.empty(2 * 4096 * batch, dtype=dt, device="cuda")
+    thff.fill_uniform(T, x, 4096 * batch, oracle.BENCH_SEED_BASE + 4099)
+    y = torch.full_like(x, float("nan"))
+    thff.ThunderFFTInitialize(T, 64)
+    dr, dc = 17, 3
+    imp = np.zeros((64, 64), dtype=np.complex64)
+    imp[dr, dc] = 1
+    thff.ThunderFFT_conv2d(T, 64, 64, x, to_device(imp, T), y, batch)
+    rows = torch.from_numpy(np.unique(np.concatenate([
+        np.arange(3), np.linspace(0, batch - 1, 16).astype(np.int64),
+        np.arange((1 << 31) // 4096 - 2, batch)]))).cuda()
+    xs = x.view(batch, 64, 64, 2).index_select(0, rows).float()
+    ys = y.view(batch, 64, 64, 2).index_select(0, rows).float()
+    want = torch.roll(xs, shifts=(dr, dc), dims=(1, 2))
+    assert bool(torch.isfinite(ys).all())
+    err = float(torch.linalg.vector_norm(ys - want) / torch.linalg.vector_norm(want))
+    print(f"{T} conv2d batch={batch}: sampled images rel_l2={err:.3e}", flush=True)
+    assert err <= TIGHT[T]
+    del x, y
+    torch.cuda.empty_cache()
