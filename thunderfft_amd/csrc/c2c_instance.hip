@@ -266,12 +266,13 @@ hipError_t launch_conv1d_valid(int precision, const void* x, long long len, cons
                                hipStream_t stream) {
     // A group is the 64 windows (one per transform slot) of one workgroup
     // pass; each workgroup transforms the filter once and walks many groups.
-    // 3 workgroups per CU (the occupancy): 2^26 values, 9 taps, 260 us fp32
-    // and 162 us fp16, against 294 / 174 us for runs of 4 groups.
+    // The occupancy in workgroups per CU: fp32 2 (with its span prefetch),
+    // fp16 3.  2^26 values, 9 taps: 232 us fp32 and 162 us fp16, against
+    // 294 / 174 us for runs of 4 groups.
     const long long valid = 65 - ntaps;
     const long long windows = (len - ntaps + 1 + valid - 1) / valid;
     const long long groups = (windows + 63) / 64 * batch;
-    const Grid g = make_grid(groups, 3, num_cus);
+    const Grid g = make_grid(groups, precision == 0 ? 2 : 3, num_cus);
     if (precision == 0)
         conv1d_valid_kernel<float2><<<g.blocks, 256, 0, stream>>>(
             static_cast<const float2*>(x), taps, static_cast<float2*>(y), len, ntaps, batch, tw,
