@@ -440,13 +440,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kValidMinWa
 
     long long g, g_end, step;
     tile_walk(groups, groups_per_block, g, g_end, step);
+    // A wave's 16 windows read 15 V + 64 values of its span; nothing past
+    // that is loaded (it is the next wave's, which may run on another XCD).
+    const int need = 15 * V + 64;
     // The span of group gg (this wave's windows) as 16-byte vectors, zero past
     // the signal's end; for signals that start on a 16-byte boundary.
     constexpr int kLoads = kSpan / (64 * kVec);
     auto span_load = [&](long long gg, W4 (&r)[kLoads]) {
         const long long bb = gg / groups_per_signal;
         const long long s0 = ((gg - bb * groups_per_signal) * P::kFPB + wave * kWindowsPerWave) * V;
-        const long long av = len - s0;
+        const long long av = len - s0 < need ? len - s0 : need;
         const IO* sp = x + bb * len + s0;
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) {
@@ -481,7 +484,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kValidMinWa
             if (g + step < g_end) span_load(g + step, next);
         }
         if (span0 >= out_len) continue;  // no window of this wave has an output
-        const long long avail = len - span0;  // > 0
+        const long long avail = len - span0 < need ? len - span0 : need;  // > 0
         const IO* src = x + b * len + span0;
         // Whole 16-byte vectors when the signal starts on one (always for b = 0).
         const bool in_vec = x16 && (b * len) % kVec == 0;
