@@ -44,10 +44,11 @@ __device__ __forceinline__ void split_rows(u32x4 lo, u32x4 hi, u32x4& r0, u32x4&
 // (2p + 1, d) as real and imaginary parts; a wave owns kFPW = 4/C transforms
 // (1024 complex values), a tile is 4 waves.  Lane l moves 8 values of both
 // rows per 16-byte step: values e = 8 l + 512 i (i = 0, 1) of the wave.
-// C = 1 (four transforms per wave, each with its own channel) needs a few
-// more registers than 4 waves per SIMD leave without spilling.
+// The spectra of a wave's transforms are kept in fp32 registers across tiles
+// (reloaded when the channels change), which holds C = 1 (four transforms per
+// wave, each with its own channel) to 2 waves per SIMD and the others to 3.
 template <int C>
-inline constexpr int kConvMfmaMinWavesPerEU = C == 1 ? 3 : 4;
+inline constexpr int kConvMfmaMinWavesPerEU = C == 1 ? 2 : 3;
 
 template <int C>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kConvMfmaMinWavesPerEU<C>))) void
@@ -76,6 +77,8 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
     const long long ntiles = (transforms + P::kFPB - 1) / P::kFPB;
     long long tile, tile_end, step;
     tile_walk(ntiles, tiles_per_block, tile, tile_end, step);
+    int spec_d = -1;  // chan[0] of the spectra spec holds
+    cpx spec[kB][4];
 
     for (; tile < tile_end; tile += step) {
         // Rows of this wave's transforms, as element offsets (-1: none).
@@ -91,11 +94,10 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
             base1[i] = tau < transforms && 2 * p + 1 < batch ? ((2 * p + 1) * channels + d) * N + k
                                                              : -1;
         }
+        // (past the last transform too: a channel is always a valid spectrum row)
 #pragma unroll
-        for (int f = 0; f < P::kFPW; ++f) {
-            const long long tau = tile * P::kFPB + wave * P::kFPW + f;
-            chan[f] = tau < transforms ? static_cast<int>(tau % channels) : 0;
-        }
+        for (int f = 0; f < P::kFPW; ++f)
+            chan[f] = static_cast<int>((tile * P::kFPB + wave * P::kFPW + f) % channels);
         u32x4 r0[2], r1[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -117,16 +119,27 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
         mfma_stage1_lds<C>(region, a, lane, v);
         mfma_steps2to6<C, true>(region, a, w1, w2, lane, v);
         // ---- product: block (f, m), lane (n, q): bin k = n + 16 m + 16C (q + 4 r) ----
+        // The spectra of the wave's transforms stay in registers while their
+        // channels do not change: they are chan[0] + f mod D, so chan[0]
+        // decides, and on a grid-stride walk whose stride in transforms is a
+        // multiple of D it never changes.
+        if (chan[0] != spec_d) {
 #pragma unroll
-        for (int b = 0; b < kB; ++b) {
-            const float2* hs = spectrum + static_cast<long long>(chan[b / C]) * N + n + 16 * (b % C) +
-                               P::kM * q;
+            for (int b = 0; b < kB; ++b) {
+                const float2* hs = spectrum + static_cast<long long>(chan[b / C]) * N + n +
+                                   16 * (b % C) + P::kM * q;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float2 hk = hs[P::kM * 4 * r];
-                v[b][r] = cmul(v[b][r], cpx{hk.x, hk.y});
+                for (int r = 0; r < 4; ++r) {
+                    const float2 hk = hs[P::kM * 4 * r];
+                    spec[b][r] = cpx{hk.x, hk.y};
+                }
             }
+            spec_d = chan[0];
         }
+#pragma unroll
+        for (int b = 0; b < kB; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], spec[b][r]);
         // ---- inverse, stage 1 straight from the registers ----
         mfma_stage1_regs<C>(ai_regs, v);
         mfma_steps2to6<C, false, true>(region, ai, w1, w2, lane, v);
@@ -299,7 +312,7 @@ __device__ __forceinline__ int xaddr4096(int k1, int t0, int t1) {
 }
 
 template <int N>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
 conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restrict__ spectrum,
                             __half* __restrict__ y, int batch, int channels,
                             const float2* __restrict__ tw, int tiles_per_block) {
@@ -370,6 +383,11 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
         }
     };
 
+    // The channel's spectrum stays in registers while the channel does not
+    // change: on a grid-stride walk whose stride is a multiple of the channel
+    // count every tile of a workgroup has the same channel.
+    long long spec_d = -1;
+    cpx spec[4][4];
     for (; tile < tile_end; tile += step) {
         const long long p = tile / channels, d = tile - p * channels;
         const long long row0 = (2 * p * channels + d) * N;
@@ -403,14 +421,21 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
         __syncthreads();
         stages23(v, a, true);
         // ---- product: bin k = 4 w + b + 16 n + 256 (q + 4 r) ----
-        const float2* hs = spectrum + d * N + 4 * wave + 16 * n + 256 * q;
+        if (d != spec_d) {  // uniform: a new channel's spectrum
+            const float2* hs = spectrum + d * N + 4 * wave + 16 * n + 256 * q;
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float2 hk = hs[b + 1024 * r];
+                    spec[b][r] = cpx{hk.x, hk.y};
+                }
+            spec_d = d;
+        }
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float2 hk = hs[b + 1024 * r];
-                v[b][r] = cmul(v[b][r], cpx{hk.x, hk.y});
-            }
+            for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], spec[b][r]);
         // ---- inverse stage 1 from the registers, then W^(t' k1') ----
 #pragma unroll
         for (int b = 0; b < 4; ++b) {

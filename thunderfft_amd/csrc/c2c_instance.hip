@@ -222,14 +222,15 @@ hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectr
     using P = C2CPlan<N>;
     const long long transforms = (static_cast<long long>(batch) + 1) / 2 * channels;
     // fp16 N = 256 ... 1024: both transforms on MFMA (fft_conv_mfma.hpp);
-    // measured against this VALU path at 2^26 samples: 63 vs 68 us (N=256),
-    // 65 vs 87 (512), 70 vs 87 (1024).  Grid: the occupancy (3 workgroups per
-    // CU for N = 256, else 4), 9-11% faster than 4 tiles per workgroup.
+    // measured against this VALU path at 2^26 samples: 61 vs 68 us (N=256),
+    // 60 vs 87 (512), 64 vs 87 (1024).  Grid: the occupancy (2 workgroups per
+    // CU for N = 256, else 3); the channels' spectra stay in registers
+    // (5-9% over reloading them per tile).
     if constexpr (N >= 256 && N <= 1024) {
         if (precision != 0) {
             using M = MfmaPlan<N / 256>;
             const long long ntiles = (transforms + M::kFPB - 1) / M::kFPB;
-            const Grid g = make_grid(ntiles, N == 256 ? 3 : 4, num_cus);
+            const Grid g = make_grid(ntiles, N == 256 ? 2 : 3, num_cus);
             conv1d_real_mfma_kernel<N / 256><<<g.blocks, 256, 0, stream>>>(
                 static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch, channels,
                 tw, g.tiles_per_block);
@@ -237,7 +238,8 @@ hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectr
         }
     }
     // fp16 N = 4096: the three-stage MFMA transform, both directions; 2
-    // workgroups per CU: 86 us against 90-102 us for 3 or 4 (2^26 samples).
+    // workgroups per CU: 77 us against 87-84 us for 3 or 4 (2^26 samples);
+    // the channel's spectrum stays in registers (84 us reloading it per tile).
     if constexpr (N == 4096) {
         if (precision != 0) {
             const Grid g = make_grid(transforms, 2, num_cus);
