@@ -288,6 +288,12 @@ __global__ __launch_bounds__(256) void conv1d_real_kernel(
     const long long ntiles = (transforms + P::kFPB - 1) / P::kFPB;
     long long tile, tile_end, step;
     tile_walk(ntiles, tiles_per_block, tile, tile_end, step);
+    // N = 4096 (one transform per tile, device-sized grids, 2 waves per SIMD
+    // already): the channel's spectrum stays in registers while the channel
+    // does not change, instead of being read from L2 per tile.
+    constexpr bool kKeepSpectrum = N == 4096;
+    long long spec_d = -1;
+    cpx spec[kKeepSpectrum ? 16 : 1];
 
     for (; tile < tile_end; tile += step) {
         // ---- both rows of each transform -> LDS as (re, im) = (row 0, row 1) ----
@@ -324,14 +330,28 @@ __global__ __launch_bounds__(256) void conv1d_real_kernel(
         for (int j = 0; j < 16; ++j) v[j] = slot[lds_pad(t + j * P::kTPF)];
 
         // ---- FFT, product with the channel's spectrum, inverse FFT ----
-        const long long tau = tile * P::kFPB + f;
-        const long long d = tau < transforms ? tau % channels : 0;
-        const float2* hs = spectrum + d * N + t;
+        // (d past the last transform too: always a valid spectrum row)
+        const long long d = (tile * P::kFPB + f) % channels;
         fft_registers<N, true>(v, slot, t, w);
+        if constexpr (kKeepSpectrum) {
+            if (d != spec_d) {
+                const float2* hs = spectrum + d * N + t;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const float2 hk = hs[j * P::kTPF];
-            v[j] = cmul(v[j], cpx{hk.x, hk.y});
+                for (int j = 0; j < 16; ++j) {
+                    const float2 hk = hs[j * P::kTPF];
+                    spec[j] = cpx{hk.x, hk.y};
+                }
+                spec_d = d;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = cmul(v[j], spec[j]);
+        } else {
+            const float2* hs = spectrum + d * N + t;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float2 hk = hs[j * P::kTPF];
+                v[j] = cmul(v[j], cpx{hk.x, hk.y});
+            }
         }
         fft_registers<N, false>(v, slot, t, w);
 
