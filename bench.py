@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmark of the hot path: batched C2C FFT, N=1024, batch 65536.
+"""Benchmark of the hot path: batched C2C FFT, N=1024, batch 65536 (the headline workload).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--cpu-seconds S]
                     [--prewarm-ms M] [--settle-ms S] [--sweep]
@@ -59,7 +59,7 @@ def parse():
                     help="per leg, after its W warm-up launches: further untimed launches of "
                          "that leg's kernel filling about this many ms before the timed ones")
     ap.add_argument("--sweep", action="store_true",
-                    help="BASELINE config 3 instead: every N at batch 2^26/N, both types and "
+                    help="the size sweep instead: every N at batch 2^26/N, both types and "
                          "directions; prints one line per case and a JSON summary")
     return ap.parse_args()
 
@@ -132,9 +132,9 @@ def time_gpu(T: str, forward: bool, steps: int, warmup: int, n: int = N_FFT,
 
 
 def time_conv(kind: str, T: str, steps: int, warmup: int) -> dict:
-    """BASELINE config 4 (conv1d: 16384 signals of 2048, per-signal complex
-    filters with N(0, 1/sqrt(2048)) taps) or config 5 (conv2d: 8192 64 x 64
-    images, one shared real filter with a N(0, 1/7) 7 x 7 corner block)."""
+    """One of the fused convolution workloads: conv1d (16384 signals of 2048,
+    per-signal complex filters with N(0, 1/sqrt(2048)) taps) or conv2d (8192
+    64 x 64 images, one shared real filter with a N(0, 1/7) 7 x 7 corner block)."""
     import numpy as np
     import torch
 
@@ -420,7 +420,7 @@ def prewarm(ms: float) -> float:
 
 
 def sweep(a) -> None:
-    """N = 64 ... 4096 at batch 2^26 / N (1 GiB fp32, 512 MiB
+    """The size sweep: N = 64 ... 4096 at batch 2^26 / N (1 GiB fp32, 512 MiB
     fp16 moved per launch), float and half, forward and inverse."""
     import thunderfft_amd as thff
 
@@ -444,8 +444,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
         print("bench.py: this build measures one GPU only; the batched transform shards "
-              "over GPUs by splitting the batch (see DESIGN.md). Run with --gpus 1.",
-              file=sys.stderr)
+              "over GPUs by splitting the batch (each rank transforms its own signals, "
+              "with no exchange). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
 

@@ -31,8 +31,8 @@ def uniform(n: int, batch: int, seed: int) -> np.ndarray:
     return np.array(vals, dtype=np.float32).view(np.complex64).reshape(batch, n)
 
 
-# (name, n, batch): config 1 of the benchmark table (N=64, batch 16) plus one
-# signal of every other length.
+# (name, n, batch): the CPU-checkable case (N=64, batch 16) plus one signal of
+# every other length.
 CASES = [("n64_b16", 64, 16)] + [(f"n{n}_b1", n, 1) for n in (128, 256, 512, 1024, 2048, 4096)]
 
 

@@ -209,14 +209,14 @@ def _large_case(T, n, batch, directions=(True, False)):
 
 @pytest.mark.parametrize("batch", [65536, 65537])
 def test_config2_n1024_float(batch):
-    """N=1024, batch 65536 (and 65537: masked partial block)."""
+    """The headline workload: N=1024, batch 65536 (and 65537: masked partial block)."""
     _large_case("float", 1024, batch)
 
 
 @pytest.mark.parametrize("T", ["float", "half"])
 @pytest.mark.parametrize("n", SIZES)
 def test_config3_sweep(T, n):
-    """batch = 2^26 / N complex values per buffer."""
+    """The size sweep: batch = 2^26 / N, so 2^26 complex values per buffer at every N."""
     _large_case(T, n, (1 << 26) // n)
 
 

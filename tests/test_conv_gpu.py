@@ -5,7 +5,7 @@ The reference gates its fused convolution on the relative L2 of the output
 against a direct circular convolution (sample/conv1d/
 conv1d_fullfft_l4096_thunder.cu:499-554, gate 5e-3).  Here: every length x
 {float, half} x {per-signal, shared filter}, batches that leave a partial last
-tile; BASELINE config 4 (16384 signals of 2048, per-signal filters) on a
+tile; the benchmarked conv1d (16384 signals of 2048, per-signal filters) on a
 subset of signals against the direct convolution, and over every signal
 through an exact property: convolving with a shifted unit impulse rolls the
 signal.
@@ -37,7 +37,7 @@ def _gpu():
 
 
 def _filters(n, count, seed):
-    """Complex taps with re, im ~ N(0, 1/sqrt(n))."""
+    """Complex taps with re, im ~ N(0, 1/sqrt(n)) (the benchmarked conv1d's filters)."""
     rng = np.random.default_rng(seed)
     h = rng.normal(0.0, 1.0 / np.sqrt(n), size=(count, n, 2)).astype(np.float32)
     return h.view(np.complex64).reshape(count, n)
@@ -79,7 +79,7 @@ def test_conv1d_matches_direct_convolution(T, n):
 
 @pytest.mark.parametrize("T", ["float", "half"])
 def test_config4_conv1d_2048(T):
-    """16384 signals of 2048, per-signal filters."""
+    """16384 signals of 2048, per-signal filters (the benchmarked conv1d)."""
     import torch
 
     import thunderfft_amd as thff
@@ -216,7 +216,7 @@ def test_conv1d_beyond_2e31_values(T):
 
 
 def _filter2d(seed, full=False):
-    """BASELINE config 5 filter: real 64 x 64, nonzero 7 x 7 corner block with
+    """The benchmarked conv2d filter: real 64 x 64, nonzero 7 x 7 corner block with
     i.i.d. N(0, 1/7) taps (full=True: every tap nonzero, complex)."""
     rng = np.random.default_rng(seed)
     h = np.zeros((64, 64), dtype=np.complex64)
@@ -248,7 +248,7 @@ def test_conv2d_matches_direct_convolution(T):
 
 
 def test_config5_conv2d_64x64():
-    """8192 float2 images of 64 x 64, shared 7 x 7-corner filter."""
+    """8192 float2 images of 64 x 64, shared 7 x 7-corner filter (the benchmarked conv2d)."""
     import torch
 
     import thunderfft_amd as thff
