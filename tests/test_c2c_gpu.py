@@ -68,8 +68,8 @@ def test_validation_matrix(T, n):
 
 @pytest.mark.parametrize("T", ["float", "half"])
 def test_golden_fixtures(T):
-    """Config 1 (N=64, batch 16, float forward) and one signal of every other
-    length against numpy.fft spectra of the fixture inputs."""
+    """The CPU-checkable case (N=64, batch 16, float forward) and one signal of
+    every other length against numpy.fft spectra of the fixture inputs."""
     g = np.load(GOLDEN)
     for key in g.files:
         if not key.endswith("_x"):

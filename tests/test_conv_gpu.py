@@ -180,10 +180,11 @@ def test_conv1d_4096_many_signals_per_workgroup(T, per_signal):
 
 @pytest.mark.parametrize("T", ["half", "float"])
 def test_conv1d_beyond_2e31_values(T):
-    """Config 4's length over 2^31 + 3 * 2048 complex values per array (x, h and
-    y: 8.6 GB each in fp16, 17 GB in fp32): signal b's filter is a unit
-    impulse at (13 b + 5) mod N, so output row b is input row b rolled by that
-    shift; checked on the first rows, a spread and every row past value 2^31."""
+    """The benchmarked conv1d's length (2048) over 2^31 + 3 * 2048 complex
+    values per array (x, h and y: 8.6 GB each in fp16, 17 GB in fp32): signal
+    b's filter is a unit impulse at (13 b + 5) mod N, so output row b is input
+    row b rolled by that shift; checked on the first rows, a spread and every
+    row past value 2^31."""
     import torch
 
     import thunderfft_amd as thff
