@@ -1,5 +1,6 @@
 """The command-line programs' argument handling on the CPU (no GPU needed):
-thff_paper_fft mirrors sample/bench/paper_fft.cu:163-170 (usage -> 2, invalid
+thff_fft mirrors sample/fft1d/main.cu:170-193 (--help -> 0, invalid arguments
+-> 1 with "FAIL: <reason>", both before any HIP call), thff_paper_fft mirrors sample/bench/paper_fft.cu:163-170 (usage -> 2, invalid
 arguments -> 1, both before any HIP call) and thff_validate_cache mirrors
 sample/validation/cache_validation.cu:160-168 (--help -> 0, anything else -> 2)."""
 import os
@@ -43,3 +44,16 @@ def test_validate_cache_arguments():
     assert r.returncode == 0 and "No FFT" in r.stdout
     r = run(p, "--bogus")
     assert r.returncode == 2 and "accepts only --help" in r.stderr
+
+
+def test_fft_quick_start_arguments():
+    p = exe("thff_fft")
+    for flag in ("--help", "-h"):
+        r = run(p, flag)
+        assert r.returncode == 0 and "[batch] [device]" in r.stdout and "5e-3" in r.stdout
+    for args, why in ((("16", "0", "1"), "too many arguments"),
+                      (("15",), "positive multiple of 16"), (("0",), "positive multiple of 16"),
+                      (("-16",), "nonnegative integer"), (("16x",), "nonnegative integer"),
+                      (("4294967296",), "nonnegative integer"), (("16", "dev"), "device must be")):
+        r = run(p, *args)
+        assert r.returncode == 1 and r.stderr.startswith("FAIL: ") and why in r.stderr, (args, r.stderr)

@@ -1,4 +1,6 @@
-"""The command-line programs on an MI355X: thff_paper_fft (the reference's
+"""The command-line programs on an MI355X: thff_fft (the reference's
+sample/fft1d/main.cu quick start: N=64 float forward vs the vendor FFT, rel
+L2 and rel Linf <= 5e-3), thff_paper_fft (the reference's
 sample/bench/paper_fft.cu timing adapter: same CSV columns, single-FFT gate
 <= 5e-3 vs an fp64 FFT, differential compute time) and thff_validate_cache
 (sample/validation/cache_validation.cu: same stages and CSV columns)."""
@@ -27,6 +29,23 @@ def exe(name):
     if not os.path.exists(path):
         raise FileNotFoundError(f"{path} missing: run __graft_entry__.build()")
     return path
+
+
+@pytest.mark.parametrize("batch", [None, 4096])
+def test_fft_quick_start_passes(batch):
+    args = [exe("thff_fft")] + ([] if batch is None else [str(batch), "0"])
+    print(" ".join(args), flush=True)
+    r = subprocess.run(args, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    lines = r.stdout.strip().splitlines()
+    assert lines[0] == (f"ThunderFFT vs hipFFT: float2, N=64, forward (unscaled), "
+                        f"batch={batch or 16}, device=0")
+    l2 = float(lines[1].split(":")[1])
+    linf = float(lines[2].split(":")[1])
+    assert lines[3].startswith("Tolerance:     5.000000e-03") and lines[4] == "PASS"
+    # both sides compute in fp32, so they agree to a few ulps
+    assert l2 <= 1e-6 and linf <= 1e-6
+    print(r.stdout, flush=True)
 
 
 # Each case moves 2^22 values and repeats the transform 50 times, so that the

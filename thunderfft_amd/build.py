@@ -89,7 +89,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     return LIB
 
 
-APPS = ("thff_validate", "thff_paper_fft", "thff_validate_cache")
+APPS = ("thff_fft", "thff_validate", "thff_paper_fft", "thff_validate_cache")
 # Shared libraries of kernels written against the public device API (tests use them).
 DEVICE_EXAMPLES = ("device_example", "bench_compute")
 
