@@ -19,14 +19,22 @@
 
 namespace thff {
 
+// Next-tile prefetch of the VALU convolutions: none; early, the next tile's
+// loads issued before the current tile is staged; or late, issued after the
+// current tile's product with the filter spectrum, before its inverse
+// transform.  Loads return in order, so a load issued after a prefetch waits
+// for it: the late form keeps the spectrum's loads ahead of the prefetch.
+enum class Prefetch { kNone, kEarly, kLate };
+
 // Waves per SIMD the fused 1-D convolution is held to (168 VGPRs for 3): 3
 // fits without spilling up to N = 2048 and measured 7-12% faster than the 2
 // the compiler picks on its own (16384 x 2048, MI355X).
 template <int N>
 inline constexpr int kConvMinWavesPerEU = N <= 2048 ? 3 : 1;
 
-template <class IO, int N, bool kPerSignal>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kConvMinWavesPerEU<N>))) void
+template <class IO, int N, bool kPerSignal, Prefetch kPf = Prefetch::kNone>
+__global__ __launch_bounds__(256) __attribute__((
+    amdgpu_waves_per_eu(kPf != Prefetch::kNone ? 2 : kConvMinWavesPerEU<N>))) void
 conv1d_kernel(const IO* __restrict__ x, const IO* __restrict__ h, IO* __restrict__ y, int batch,
               const float2* __restrict__ tw, int tiles_per_block) {
     using P = C2CPlan<N>;
@@ -54,9 +62,29 @@ conv1d_kernel(const IO* __restrict__ x, const IO* __restrict__ h, IO* __restrict
         for (int j = 0; j < 16; ++j) hs[j] = {hs[j].re * kScale, hs[j].im * kScale};
     }
 
+    // Prefetch::kEarly: the next tile's raw signal (and filter) load while
+    // the current tile is transformed.
+    constexpr bool kPrefetch = kPf == Prefetch::kEarly;
+    typename T::Raw nx, nh;
+    if constexpr (kPrefetch) {
+        io.load(nx, x, tile, batch);
+        if constexpr (kPerSignal) io.load(nh, h, tile, batch);
+    }
     for (; tile < tile_end; tile += step) {
         cpx v[16];
-        if constexpr (kPerSignal) {
+        if constexpr (kPrefetch) {
+            typename T::Raw rx = nx, rh;
+            if constexpr (kPerSignal) rh = nh;
+            if (tile + step < tile_end) {
+                io.load(nx, x, tile + step, batch);
+                if constexpr (kPerSignal) io.load(nh, h, tile + step, batch);
+            }
+            if constexpr (kPerSignal) {
+                io.stage(rh, hs);
+                fft_registers<N, true>(hs, io.slot, io.t, w);
+            }
+            io.stage(rx, v);
+        } else if constexpr (kPerSignal) {
             // The filter first, so its raw tile is dead before the signal's
             // arrives; float2 issues the signal's loads before transforming
             // the filter, half2 (tighter on registers) after.
@@ -261,7 +289,7 @@ __global__ __launch_bounds__(256) void conv1d_real_filter_kernel(const float* __
     }
 }
 
-template <class IO, int N>
+template <class IO, int N, Prefetch kPf = Prefetch::kNone>
 __global__ __launch_bounds__(256) void conv1d_real_kernel(
     const typename RealIo<IO>::S* __restrict__ x, const float2* __restrict__ spectrum,
     typename RealIo<IO>::S* __restrict__ y, int batch, int channels,
@@ -292,28 +320,105 @@ __global__ __launch_bounds__(256) void conv1d_real_kernel(
     // already): the channel's spectrum stays in registers while the channel
     // does not change, instead of being read from L2 per tile.
     constexpr bool kKeepSpectrum = N == 4096;
-    long long spec_d = -1;
+    int spec_d = -1;
     cpx spec[kKeepSpectrum ? 16 : 1];
+
+    // Position of a tile's first transform tau = tl * kFPB as pair p and
+    // channel d (tau = p * channels + d).  Successive tiles of the walk are
+    // step * kFPB = adv_p * channels + adv_d transforms apart, so positions
+    // advance without a 64-bit division per tile; transform k of a tile sits
+    // at channel (d + k) mod channels of pair p + (d + k) / channels (32-bit).
+    struct Pos {
+        long long p;
+        int d;
+    };
+    const long long adv = step * P::kFPB;
+    const long long adv_p = adv / channels;
+    const int adv_d = static_cast<int>(adv - adv_p * channels);
+    Pos pos;
+    pos.p = tile * P::kFPB / channels;
+    pos.d = static_cast<int>(tile * P::kFPB - pos.p * channels);
+    auto advance = [&](Pos q) {
+        q.p += adv_p;
+        q.d += adv_d;
+        if (q.d >= channels) q.d -= channels, ++q.p;
+        return q;
+    };
+    auto locate = [&](Pos q, int k, long long& pair, int& chan) {
+        const unsigned s = static_cast<unsigned>(q.d) + static_cast<unsigned>(k);
+        const unsigned c = static_cast<unsigned>(channels);
+        const unsigned j = s / c;
+        pair = q.p + j;
+        chan = static_cast<int>(s - j * c);
+    };
+
+    // This lane's kSteps 16-byte pieces of tile tl in both rows.  Piece i is
+    // tile element e = u_i + kVec lane, u_i = 1024 wave + 64 kVec i: element
+    // e % N of transform tl * kFPB + e / N.  For N >= 64 kVec the 64 lanes'
+    // pieces i lie in one transform, so the row offsets of u_i are
+    // wave-uniform (scalar) and a lane adds kVec lane; for N >= 1024 a wave's
+    // 1024 elements lie in one transform and one offset per row serves every
+    // piece.  Shorter transforms keep per-lane offsets.  -1: no such row.
+    constexpr bool kUniform = N >= 64 * kVec;
+    constexpr int kRowOffsets = N >= 1024 ? 1 : kSteps;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    struct Rows {
+        long long o0[kRowOffsets], o1[kRowOffsets];
+        u32x4 r0[kSteps], r1[kSteps];
+    };
+    auto piece = [&](const long long* o, int i) -> long long {
+        if constexpr (N >= 1024)
+            return o[0] < 0 ? -1 : o[0] + 64 * kVec * i + kVec * lane;
+        else if constexpr (kUniform)
+            return o[i] < 0 ? -1 : o[i] + kVec * lane;
+        else
+            return o[i];
+    };
+    auto fetch = [&](long long tl, Pos q, Rows& rw) {
+#pragma unroll
+        for (int i = 0; i < kRowOffsets; ++i) {
+            const int e = kUniform ? 1024 * wave_u + (N >= 1024 ? 0 : 64 * kVec * i)
+                                   : 1024 * wave + kVec * lane + 64 * kVec * i;
+            const int k = e / N;
+            const long long tau = tl * P::kFPB + k;
+            long long pair;
+            int chan;
+            locate(q, k, pair, chan);
+            const long long b0 = 2 * pair, b1 = b0 + 1;
+            const int n = e % N;
+            rw.o0[i] = tau < transforms ? (b0 * channels + chan) * N + n : -1;
+            rw.o1[i] = tau < transforms && b1 < batch ? (b1 * channels + chan) * N + n : -1;
+        }
+#pragma unroll
+        for (int i = 0; i < kSteps; ++i) {
+            const long long a0 = piece(rw.o0, i), a1 = piece(rw.o1, i);
+            rw.r0[i] = a0 >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + a0)) : u32x4{};
+            rw.r1[i] = a1 >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + a1)) : u32x4{};
+        }
+    };
+    // The next tile's pieces load while the current tile is transformed
+    // (kPf): early, right after the current tile's pieces are taken, or
+    // late, after its product with the spectrum.
+    Rows next;
+    if constexpr (kPf != Prefetch::kNone)
+        if (tile < tile_end) fetch(tile, pos, next);
 
     for (; tile < tile_end; tile += step) {
         // ---- both rows of each transform -> LDS as (re, im) = (row 0, row 1) ----
-        long long base0[kSteps], base1[kSteps];  // element offsets, -1 = no row
+        Rows cur;
+        const Pos at = pos;
+        pos = advance(pos);
+        if constexpr (kPf == Prefetch::kEarly) {
+            cur = next;
+            if (tile + step < tile_end) fetch(tile + step, pos, next);
+        } else if constexpr (kPf == Prefetch::kLate) {
 #pragma unroll
-        for (int i = 0; i < kSteps; ++i) {
-            const int e = 1024 * wave + kVec * lane + 64 * kVec * i;
-            const long long tau = tile * P::kFPB + e / N;
-            const long long p = tau / channels, d = tau - p * channels;
-            const long long b0 = 2 * p, b1 = b0 + 1;
-            const int n = e % N;
-            base0[i] = tau < transforms ? (b0 * channels + d) * N + n : -1;
-            base1[i] = tau < transforms && b1 < batch ? (b1 * channels + d) * N + n : -1;
+            for (int i = 0; i < kRowOffsets; ++i) cur.o0[i] = next.o0[i], cur.o1[i] = next.o1[i];
+        } else {
+            fetch(tile, at, cur);
         }
-        u32x4 r0[kSteps], r1[kSteps];
-#pragma unroll
-        for (int i = 0; i < kSteps; ++i) {
-            r0[i] = base0[i] >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + base0[i])) : u32x4{};
-            r1[i] = base1[i] >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + base1[i])) : u32x4{};
-        }
+        const u32x4* r0 = kPf == Prefetch::kLate ? next.r0 : cur.r0;
+        const u32x4* r1 = kPf == Prefetch::kLate ? next.r1 : cur.r1;
         region_sync<P::kWaveLocal>();
 #pragma unroll
         for (int i = 0; i < kSteps; ++i) {
@@ -330,12 +435,14 @@ __global__ __launch_bounds__(256) void conv1d_real_kernel(
         for (int j = 0; j < 16; ++j) v[j] = slot[lds_pad(t + j * P::kTPF)];
 
         // ---- FFT, product with the channel's spectrum, inverse FFT ----
-        // (d past the last transform too: always a valid spectrum row)
-        const long long d = (tile * P::kFPB + f) % channels;
+        // (a channel past the last transform too: always a valid spectrum row)
+        long long pair_f;
+        int d;
+        locate(at, f, pair_f, d);
         fft_registers<N, true>(v, slot, t, w);
         if constexpr (kKeepSpectrum) {
             if (d != spec_d) {
-                const float2* hs = spectrum + d * N + t;
+                const float2* hs = spectrum + static_cast<long long>(d) * N + t;
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
                     const float2 hk = hs[j * P::kTPF];
@@ -346,13 +453,15 @@ __global__ __launch_bounds__(256) void conv1d_real_kernel(
 #pragma unroll
             for (int j = 0; j < 16; ++j) v[j] = cmul(v[j], spec[j]);
         } else {
-            const float2* hs = spectrum + d * N + t;
+            const float2* hs = spectrum + static_cast<long long>(d) * N + t;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 const float2 hk = hs[j * P::kTPF];
                 v[j] = cmul(v[j], cpx{hk.x, hk.y});
             }
         }
+        if constexpr (kPf == Prefetch::kLate)
+            if (tile + step < tile_end) fetch(tile + step, pos, next);
         fft_registers<N, false>(v, slot, t, w);
 
         // ---- real part -> row 0, imaginary part -> row 1 ----
@@ -369,8 +478,9 @@ __global__ __launch_bounds__(256) void conv1d_real_kernel(
                 const cpx z = lds[lds_pad(e + c)];
                 a[c] = z.re, b[c] = z.im;
             }
-            if (base0[i] >= 0) st_nt(reinterpret_cast<u32x4*>(y + base0[i]), R::encode(a));
-            if (base1[i] >= 0) st_nt(reinterpret_cast<u32x4*>(y + base1[i]), R::encode(b));
+            const long long a0 = piece(cur.o0, i), a1 = piece(cur.o1, i);
+            if (a0 >= 0) st_nt(reinterpret_cast<u32x4*>(y + a0), R::encode(a));
+            if (a1 >= 0) st_nt(reinterpret_cast<u32x4*>(y + a1), R::encode(b));
         }
     }
 }

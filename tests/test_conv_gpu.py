@@ -178,6 +178,45 @@ def test_conv1d_4096_many_signals_per_workgroup(T, per_signal):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("n", SIZES)
+@pytest.mark.parametrize("per_signal", [True, False])
+def test_conv1d_grid_stride_walks(T, n, per_signal):
+    """2^25 values plus a partial tile: 8192 tiles of 4096 values, more than
+    twice any device-sized grid (at most 16 workgroups per CU), so every
+    workgroup convolves several tiles in turn, prefetching the next one where
+    the launch shape does.  Every signal through the impulse roll."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    fpb = thff.transforms_per_block(n)
+    batch = (1 << 25) // n + fpb // 2 + 1
+    dt = torch.float32 if T == "float" else torch.float16
+    x = torch.empty(2 * n * batch, dtype=dt, device="cuda")
+    thff.fill_uniform(T, x, n * batch, oracle.BENCH_SEED_BASE + 3 * n + per_signal)
+    y = torch.full_like(x, float("nan"))
+    thff.ThunderFFTInitialize(T, n)
+    nh = batch if per_signal else 1
+    shifts = (7 * np.arange(nh) + 3) % n
+    imp = torch.zeros(nh, n, 2, dtype=dt, device="cuda")
+    imp[torch.arange(nh, device="cuda"), torch.from_numpy(shifts).cuda(), 0] = 1
+    print(f"{T} conv1d N={n} batch={batch} {'per-signal' if per_signal else 'shared'}", flush=True)
+    thff.ThunderFFT_conv1d(T, n, x, imp, y, batch, per_signal)
+    xs = x.view(batch, n, 2).float()
+    s = torch.from_numpy(np.broadcast_to(shifts, (batch,)).copy()).cuda()
+    idx = (torch.arange(n, device="cuda")[None, :] - s[:, None]) % n
+    want = torch.gather(xs, 1, idx[:, :, None].expand(batch, n, 2))
+    got = y.view(batch, n, 2).float()
+    assert bool(torch.isfinite(got).all())
+    err = float(torch.linalg.vector_norm(got - want) / torch.linalg.vector_norm(want))
+    worst = float((got - want).abs().max())
+    print(f"  impulse roll rel_l2={err:.3e} max={worst:.3e}", flush=True)
+    assert err <= TIGHT[T] and worst <= (5e-3 if T == "half" else 1e-5)
+    del x, y, imp, xs, want, got
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("T", ["half", "float"])
 def test_conv1d_beyond_2e31_values(T):
     """The benchmarked conv1d's length (2048) over 2^31 + 3 * 2048 complex

@@ -192,14 +192,16 @@ def test_async_equals_sync_and_scale(T):
 
 @pytest.mark.parametrize("T", ["float", "half"])
 @pytest.mark.parametrize("n,batch,channels", [(1024, 255, 257), (4096, 33, 64), (4096, 401, 3),
-                                               (1024, 2801, 5), (512, 2601, 5), (256, 2401, 7)])
+                                               (1024, 2801, 5), (512, 2601, 5), (256, 2401, 7),
+                                               (64, 2403, 61), (128, 2403, 31), (2048, 803, 11)])
 def test_full_size_impulse_rolls(T, n, batch, channels):
     """Filter d is a unit impulse at tap s_d = (17 d + 1) mod N, so every output
-    row is its input row rolled by s_d (checked over all signals).  The last
-    four cases have more tiles than a 256-CU device's grid (512 or 768
-    workgroups), and channel counts that do not divide the grid's stride in
-    transforms, so a workgroup's tiles change channel and a kept spectrum must
-    be reloaded."""
+    row is its input row rolled by s_d (checked over all signals).  All but the
+    first two cases have more tiles than a 256-CU device's grid (512 to 1024
+    workgroups), so workgroups walk several tiles (prefetching the next one
+    where the launch shape does), with channel counts that do not divide the
+    grid's stride in transforms: a workgroup's tiles change channel and pair,
+    and a kept spectrum must be reloaded."""
     import torch
 
     import thunderfft_amd as thff

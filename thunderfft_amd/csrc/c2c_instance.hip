@@ -123,25 +123,49 @@ hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, in
     return hipGetLastError();
 }
 
-// VALU convolution grids (conv1d_kernel, conv1d_real_kernel): fp32 up to
-// N = 1024 one tile per workgroup (127-175 us against 134-181 us for the best
-// device grid); otherwise the kernel's occupancy: N = 2048 3 per CU (fp32
-// conv1d 163 us against 172 us for two tiles per workgroup; fp16 real 111 vs
-// 121 us), N = 4096 2 per CU (174 vs 180 us; real 184 vs 195 us), fp16
-// N = 64, 128 4 per CU (real 64 vs 68 us) or 16 (conv1d 82-87 vs 85-91 us).
+// Launch shapes of the VALU convolutions (conv1d_kernel, conv1d_real_kernel):
+// workgroups per CU (make_grid; 0 = one tile per workgroup) and next-tile
+// prefetch.  Measured on MI355X (complex: 2^25 values per array; real: 2^26
+// samples, 64 channels):
+//   complex fp32, per-signal filters: one tile per workgroup up to N = 1024
+//     (127-144 us against 134-181 us for device grids, prefetch 138-152);
+//     N = 2048 3 per CU (160 us; 2 tiles per workgroup 172, prefetch 163);
+//     N = 4096 2 per CU (167 us; prefetch 192).
+//   complex fp32, shared filter (transformed once per workgroup): one tile
+//     per workgroup up to N = 256 (92-96 us, equal to prefetch); N = 512 2
+//     per CU with early prefetch (101 us, one tile per workgroup 122);
+//     N = 1024, 2048 3 per CU (102 and 107 us; one tile per workgroup 127);
+//     N = 4096 2 per CU with early prefetch (113 us against 121).
+//   real fp32: 2 per CU with prefetch, late up to N = 512 and early above:
+//     97-116 us for N = 64 ... 512 (one tile per workgroup 110-153) and
+//     112/121/115 us for N = 1024/2048/4096 (168-176 without prefetch).
+//   fp16 on VALU (N = 64, 128; real also N = 2048, complex N <= 128 only):
+//     real 4 per CU (62-64 us; prefetch 62-74) and 3 at N = 2048 (102 us;
+//     prefetch 124), complex 16 per CU (conv1d 78-87 us against 85-91).
+struct ConvShape {
+    int per_cu;
+    Prefetch prefetch;
+};
+
 template <int N>
-constexpr int valu_conv_per_cu(int precision, bool real) {
-    if (N >= 2048) return N == 2048 ? 3 : 2;
-    if (precision == 0) return 0;
-    return real ? 4 : 16;
+constexpr ConvShape valu_conv_shape(int precision, bool real, bool per_signal) {
+    if (precision != 0) return {real ? (N == 2048 ? 3 : 4) : 16, Prefetch::kNone};
+    if (real) return {2, N <= 512 ? Prefetch::kLate : Prefetch::kEarly};
+    if (per_signal) return {N <= 1024 ? 0 : N == 2048 ? 3 : 2, Prefetch::kNone};
+    if (N <= 256) return {0, Prefetch::kNone};
+    if (N == 512 || N == 4096) return {2, Prefetch::kEarly};
+    return {3, Prefetch::kNone};
 }
 
 template <class IO, int N>
-void enqueue_conv1d(bool per_signal, Grid g, const IO* x, const IO* h, IO* y, int batch,
-                    const float2* tw, hipStream_t stream) {
+void enqueue_conv1d(bool per_signal, Grid g, Prefetch pf, const IO* x, const IO* h, IO* y,
+                    int batch, const float2* tw, hipStream_t stream) {
     if (per_signal)
         conv1d_kernel<IO, N, true><<<g.blocks, 256, 0, stream>>>(x, h, y, batch, tw,
                                                                  g.tiles_per_block);
+    else if (pf == Prefetch::kEarly)
+        conv1d_kernel<IO, N, false, Prefetch::kEarly><<<g.blocks, 256, 0, stream>>>(
+            x, h, y, batch, tw, g.tiles_per_block);
     else
         conv1d_kernel<IO, N, false><<<g.blocks, 256, 0, stream>>>(x, h, y, batch, tw,
                                                                   g.tiles_per_block);
@@ -194,15 +218,16 @@ hipError_t launch_conv1d(int precision, bool per_signal_filter, const void* x, c
     }
     using P = C2CPlan<N>;
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
-    const Grid g = make_grid(ntiles, valu_conv_per_cu<N>(precision, false), num_cus);
+    const ConvShape shape = valu_conv_shape<N>(precision, false, per_signal_filter);
+    const Grid g = make_grid(ntiles, shape.per_cu, num_cus);
     if (precision == 0)
-        enqueue_conv1d<float2, N>(per_signal_filter, g, static_cast<const float2*>(x),
-                                  static_cast<const float2*>(h), static_cast<float2*>(y), batch, tw,
-                                  stream);
+        enqueue_conv1d<float2, N>(per_signal_filter, g, shape.prefetch,
+                                  static_cast<const float2*>(x), static_cast<const float2*>(h),
+                                  static_cast<float2*>(y), batch, tw, stream);
     else
-        enqueue_conv1d<__half2, N>(per_signal_filter, g, static_cast<const __half2*>(x),
-                                   static_cast<const __half2*>(h), static_cast<__half2*>(y), batch,
-                                   tw, stream);
+        enqueue_conv1d<__half2, N>(per_signal_filter, g, Prefetch::kNone,
+                                   static_cast<const __half2*>(x), static_cast<const __half2*>(h),
+                                   static_cast<__half2*>(y), batch, tw, stream);
     return hipGetLastError();
 }
 
@@ -250,9 +275,11 @@ hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectr
         }
     }
     const long long ntiles = (transforms + P::kFPB - 1) / P::kFPB;
-    const Grid g = make_grid(ntiles, valu_conv_per_cu<N>(precision, true), num_cus);
+    const ConvShape shape = valu_conv_shape<N>(precision, true, false);
+    const Grid g = make_grid(ntiles, shape.per_cu, num_cus);
+    constexpr Prefetch kF32 = valu_conv_shape<N>(0, true, false).prefetch;
     if (precision == 0)
-        conv1d_real_kernel<float2, N><<<g.blocks, 256, 0, stream>>>(
+        conv1d_real_kernel<float2, N, kF32><<<g.blocks, 256, 0, stream>>>(
             static_cast<const float*>(x), spectrum, static_cast<float*>(y), batch, channels, tw,
             g.tiles_per_block);
     else
