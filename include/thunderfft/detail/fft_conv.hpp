@@ -125,86 +125,207 @@ namespace thff {
 // conv2d: y[b] = IFFT2(FFT2(x[b]) * FFT2(h)) / (64*64) for 64 x 64 row-major
 // images and one shared 64 x 64 filter h, i.e. the 2-D circular convolution
 // y[b][r][c] = sum x[b][r'][c'] * h[(r - r') mod 64][(c - c') mod 64].
+// Reference: sample/conv2d/thunder.cu:70-207 (row FFT, column FFT x H, column
+// IFFT, row IFFT as three launches over a 1024 x 1024 image) and the unbuilt
+// 64 x 64 tile sketch sample/conv2d/thunder_tile64.cu:33-208.
 //
-// One image is one 4096-value tile.  Rows are 64-point transforms (transform
-// slot f = row, lane t holds columns t + 4j).  A workgroup-wide LDS transpose
-// writes row f's element c into column transform c's slot at position f, so
-// the column transforms run with the same 64-point machinery; the product
-// with the filter spectrum (computed once per workgroup by the same steps,
-// so its lane layout matches) and the inverse column transforms stay in
-// registers, then the transpose runs back and the inverse row transforms
-// finish.  Reference: sample/conv2d/thunder.cu:70-207 (row FFT, column FFT x H
-// x column IFFT, row IFFT as three launches over a 1024 x 1024 image) and
-// the unbuilt 64 x 64 tile sketch sample/conv2d/thunder_tile64.cu:33-208.
+// One image is one workgroup tile.  Both indices split as r = r0 + 4 r1,
+// c = c0 + 4 c1 (r0, c0 < 4; r1, c1 < 16), and the 2-D DFT runs as four
+// stages, two 16-point and two 4-point ones, in three lane layouts:
+//   L0  wave r0, lane c:            v[r1]  = x[r0 + 4 r1][c]
+//       DFT16 over r1 -> kr1; wave-local LDS exchange E1 ->
+//   L1  wave r0, lane (c0, kr1):    v[c1]
+//       DFT16 over c1 -> kc1; workgroup LDS exchange E2 ->
+//   L2  lane (kr1, kc1):            v[4 r0 + c0]
+//       twiddles W64^(c0 kc1), DFT4 over c0; W64^(r0 kr1), DFT4 over r0:
+//       v[4 kr0 + kc0] = X[kr1 + 16 kr0][kc1 + 16 kc0].
+// The filter spectrum is built by the same steps once per workgroup, so the
+// product is lane-local, and the inverse runs the stages backwards through
+// the same layouts (X[k][l] -> exp(+2 pi i (r k + c l)/64) factors the same
+// way).  Loads and stores move whole rows: in L0 one instruction of a wave
+// reads or writes 64 consecutive values of row r0 + 4 r1, so images go from
+// HBM to registers and back with no staging, and a 2-D transform takes two
+// LDS exchanges (the row/column form takes three plus the staging).
 // ---------------------------------------------------------------------------
+namespace conv2d {
+// E1: per-wave region, row kr1 of 64 values at kr1 * kE1 (66 = 2 mod 32
+// 8-byte words: the L1 reads of 32 lanes (c0 in {0,1} or {2,3}, kr1 < 16) hit
+// 32 distinct word positions mod 32, i.e. all 64 banks once).
+inline constexpr int kE1 = 66;
+inline constexpr int kE1Wave = 16 * kE1;
+// E2: value (r0, c0, kr1, kc1) at (4 r0 + c0) * kM + 17 kr1 + kc1.  L1 writes
+// of 32 lanes (c0 parity fixed, kr1 < 16) land on 17 kr1 + 16 c0 mod 32, all
+// distinct; L2 reads of 32 lanes (two kr1, kc1 < 16) share one word position.
+inline constexpr int kM = 272;
+inline constexpr int kLds = 16 * kM > 4 * kE1Wave ? 16 * kM : 4 * kE1Wave;
 
-// Rows <-> columns of the 64 x 64 tile held as v[j] = A[f][t + 4j].
-__device__ __forceinline__ void transpose64(cpx (&v)[16], cpx* lds, int f, int t) {
-    using P = C2CPlan<64>;
-    __syncthreads();
+// The lane's twiddle bases (positive angle, conjugated at use for forward):
+// wr[i] = W64^((i + 1) kr1), wc[i] = W64^((i + 1) kc1) of its L2 position.
+struct Twiddles {
+    cpx wr[3], wc[3];
+    __device__ __forceinline__ void load(int tid, const float2* __restrict__ tw) {
+        const int kr1 = tid >> 4, kc1 = tid & 15;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) lds[(t + 4 * j) * P::kSlot + lds_pad(f)] = v[j];
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = lds[f * P::kSlot + lds_pad(t + 4 * j)];
-}
+        for (int i = 0; i < 3; ++i) {
+            const float2 a = tw[((i + 1) * kr1) & 63], b = tw[((i + 1) * kc1) & 63];
+            wr[i] = {a.x, a.y};
+            wc[i] = {b.x, b.y};
+        }
+    }
+};
 
-// v[j] = A[f][t + 4j] -> v[j] = X[kr = t + 4j][kc = f] (transposed spectrum).
 template <bool FWD>
-__device__ __forceinline__ void fft2_64(cpx (&v)[16], cpx* lds, cpx* slot, int f, int t,
-                                        const LaneTwiddles<64>& w) {
-    fft_registers<64, FWD>(v, slot, t, w);  // rows
-    transpose64(v, lds, f, t);
-    fft_registers<64, FWD>(v, slot, t, w);  // columns
+__device__ __forceinline__ cpx twiddle(cpx a, cpx w) {
+    return FWD ? cmulc(a, w) : cmul(a, w);
 }
 
-// The inverse of fft2_64's layout change: transposed spectrum in, image out.
-__device__ __forceinline__ void ifft2_64(cpx (&v)[16], cpx* lds, cpx* slot, int f, int t,
-                                         const LaneTwiddles<64>& w) {
-    fft_registers<64, false>(v, slot, t, w);  // columns
-    transpose64(v, lds, f, t);
-    fft_registers<64, false>(v, slot, t, w);  // rows
+// DFT4 over c0 (stride 1 in v) for every r0, or over r0 (stride 4) for every c0.
+template <bool FWD, int kStride, int kStep>
+__device__ __forceinline__ void dft4s(cpx (&v)[16]) {
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+        cpx t[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t[i] = v[o * kStep + i * kStride];
+        Dft<4, FWD>::run(t);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[o * kStep + i * kStride] = t[i];
+    }
+}
+
+// L0 image -> L2 spectrum.
+__device__ __forceinline__ void forward(cpx (&v)[16], cpx* lds, int tid, const Twiddles& w) {
+    const int wave = tid >> 6, lane = tid & 63, c0 = lane >> 4, kr1 = lane & 15;
+    cpx* e1 = lds + wave * kE1Wave;
+    Dft<16, true>::run(v);  // over r1
+#pragma unroll
+    for (int k = 0; k < 16; ++k) e1[k * kE1 + lane] = v[k];
+    wave_lds_sync();
+#pragma unroll
+    for (int c1 = 0; c1 < 16; ++c1) v[c1] = e1[kr1 * kE1 + c0 + 4 * c1];
+    Dft<16, true>::run(v);  // over c1
+    __syncthreads();        // every wave is done with its E1 reads
+    cpx* m = lds + (4 * wave + c0) * kM + 17 * kr1;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) m[k] = v[k];
+    __syncthreads();
+    const cpx* q = lds + 17 * (tid >> 4) + (tid & 15);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = q[i * kM];
+#pragma unroll
+    for (int r0 = 0; r0 < 4; ++r0)
+#pragma unroll
+        for (int c0_ = 1; c0_ < 4; ++c0_) v[4 * r0 + c0_] = twiddle<true>(v[4 * r0 + c0_], w.wc[c0_ - 1]);
+    dft4s<true, 1, 4>(v);  // over c0
+#pragma unroll
+    for (int r0 = 1; r0 < 4; ++r0)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[4 * r0 + k] = twiddle<true>(v[4 * r0 + k], w.wr[r0 - 1]);
+    dft4s<true, 4, 1>(v);  // over r0
+}
+
+// L2 spectrum -> L0 image (unnormalized inverse).  The caller's next LDS use
+// must follow a __syncthreads() or be this wave's own E1 region.
+__device__ __forceinline__ void inverse(cpx (&v)[16], cpx* lds, int tid, const Twiddles& w) {
+    const int wave = tid >> 6, lane = tid & 63, c0 = lane >> 4, kr1 = lane & 15;
+    dft4s<false, 4, 1>(v);  // over kr0
+#pragma unroll
+    for (int r0 = 1; r0 < 4; ++r0)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[4 * r0 + k] = twiddle<false>(v[4 * r0 + k], w.wr[r0 - 1]);
+    dft4s<false, 1, 4>(v);  // over kc0
+#pragma unroll
+    for (int r0 = 0; r0 < 4; ++r0)
+#pragma unroll
+        for (int c0_ = 1; c0_ < 4; ++c0_) v[4 * r0 + c0_] = twiddle<false>(v[4 * r0 + c0_], w.wc[c0_ - 1]);
+    __syncthreads();  // every wave is done with its E2 reads
+    cpx* q = lds + 17 * (tid >> 4) + (tid & 15);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q[i * kM] = v[i];
+    __syncthreads();
+    const cpx* m = lds + (4 * wave + c0) * kM + 17 * kr1;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = m[k];
+    Dft<16, false>::run(v);  // over kc1
+    __syncthreads();         // every wave is done with its E2' reads
+    cpx* e1 = lds + wave * kE1Wave;
+#pragma unroll
+    for (int c1 = 0; c1 < 16; ++c1) e1[kr1 * kE1 + c0 + 4 * c1] = v[c1];
+    wave_lds_sync();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = e1[k * kE1 + lane];
+    Dft<16, false>::run(v);  // over kr1
+}
+
+// Image `img` of `base` in L0, as loaded (raw[r1] = base[img][wave + 4 r1][lane])
+// and decoded to v[r1].
+template <class IO>
+struct Raw {
+    typename Io<IO>::W1 w[16];
+};
+
+template <class IO>
+__device__ __forceinline__ void load(Raw<IO>& r, const IO* __restrict__ base, long long img,
+                                     int tid) {
+    using W = typename Io<IO>::W1;
+    const W* p = reinterpret_cast<const W*>(base + img * 4096) + tid;
+#pragma unroll
+    for (int r1 = 0; r1 < 16; ++r1) r.w[r1] = ld_nt(p + 256 * r1);
 }
 
 template <class IO>
-__global__ __launch_bounds__(256) void conv2d64_kernel(const IO* __restrict__ x,
-                                                       const IO* __restrict__ h,
-                                                       IO* __restrict__ y, int batch,
-                                                       const float2* __restrict__ tw,
-                                                       int tiles_per_block) {
-    using P = C2CPlan<64>;
-    using T = TileIO<IO, 64>;
-    __shared__ cpx lds[P::kLdsSlots];
-    const T io(lds, threadIdx.x);
+__device__ __forceinline__ void decode(const Raw<IO>& r, cpx (&v)[16]) {
+#pragma unroll
+    for (int r1 = 0; r1 < 16; ++r1) v[r1] = Io<IO>::decode1(r.w[r1]);
+}
 
-    LaneTwiddles<64> w;
-    w.load(io.t, tw);
+template <class IO>
+__device__ __forceinline__ void store(const cpx (&v)[16], IO* __restrict__ base, long long img,
+                                      int tid) {
+    using W = typename Io<IO>::W1;
+    W* p = reinterpret_cast<W*>(base + img * 4096) + tid;
+#pragma unroll
+    for (int r1 = 0; r1 < 16; ++r1) st_nt(p + 256 * r1, Io<IO>::encode1(v[r1]));
+}
+}  // namespace conv2d
+
+// The next image's loads are issued before the current image is transformed.
+// Held to 4 waves per SIMD (4 workgroups per CU): the fp32 kernel then keeps 2
+// dwords in scratch.  Measured on MI355X, 8192 fp32 images: 101-104 us,
+// against 103-106 us at its natural 129 VGPRs (3 per CU) and 104-107 us
+// without the prefetch.
+template <class IO>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void
+conv2d64_kernel(const IO* __restrict__ x, const IO* __restrict__ h, IO* __restrict__ y,
+                int batch, const float2* __restrict__ tw, int tiles_per_block) {
+    __shared__ cpx lds[conv2d::kLds];
+    const int tid = threadIdx.x;
+    conv2d::Twiddles w;
+    w.load(tid, tw);
     constexpr float kScale = 1.0f / 4096.0f;
 
-    long long tile, tile_end, step;
-    tile_walk(batch, tiles_per_block, tile, tile_end, step);
-    if (tile >= tile_end) return;  // uniform over the workgroup
+    long long img, img_end, step;
+    tile_walk(batch, tiles_per_block, img, img_end, step);
+    if (img >= img_end) return;  // uniform over the workgroup
 
-    cpx hs[16];  // FFT2(h) / 4096 in the transposed-spectrum layout
-    {
-        typename T::Raw r;
-        io.load(r, h, 0, 64);
-        io.stage(r, hs);
-        fft2_64<true>(hs, lds, io.slot, io.f, io.t, w);
+    conv2d::Raw<IO> raw;
+    cpx hs[16];  // FFT2(h) / 4096 in the L2 layout
+    conv2d::load(raw, h, 0, tid);
+    conv2d::decode(raw, hs);
+    conv2d::load(raw, x, img, tid);
+    conv2d::forward(hs, lds, tid, w);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) hs[j] = {hs[j].re * kScale, hs[j].im * kScale};
-    }
-    const long long rows = 64LL * batch;  // TileIO counts 64-point row transforms
-    for (; tile < tile_end; tile += step) {
-        typename T::Raw r;
-        io.load(r, x, tile, rows);
+    for (int i = 0; i < 16; ++i) hs[i] = {hs[i].re * kScale, hs[i].im * kScale};
+    __syncthreads();  // the filter's E2 reads are done before the first E1 writes
+    for (; img < img_end; img += step) {
         cpx v[16];
-        io.stage(r, v);
-        fft2_64<true>(v, lds, io.slot, io.f, io.t, w);
+        conv2d::decode(raw, v);
+        if (img + step < img_end) conv2d::load(raw, x, img + step, tid);
+        conv2d::forward(v, lds, tid, w);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = cmul(v[j], hs[j]);
-        ifft2_64(v, lds, io.slot, io.f, io.t, w);
-        io.store(v, y, tile, rows);
+        for (int i = 0; i < 16; ++i) v[i] = cmul(v[i], hs[i]);
+        conv2d::inverse(v, lds, tid, w);
+        conv2d::store(v, y, img, tid);
     }
 }
 

@@ -315,9 +315,9 @@ hipError_t launch_conv1d_valid(int precision, const void* x, long long len, cons
 
 hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y, int batch,
                            const float2* tw, int num_cus, hipStream_t stream) {
-    // One image per tile; each workgroup transforms the filter once.  4
-    // workgroups per CU (the occupancy): fp32 120 us, fp16 101 us for 8192
-    // images, against 127 / 104 us for 8 images per workgroup.
+    // One image per tile; a device grid of 4 workgroups per CU (the kernel's
+    // occupancy) walks the images grid-stride, and each workgroup transforms
+    // the filter once.
     const Grid g = make_grid(batch, 4, num_cus);
     if (precision == 0)
         conv2d64_kernel<float2><<<g.blocks, 256, 0, stream>>>(
