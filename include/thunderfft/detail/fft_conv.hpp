@@ -32,7 +32,10 @@ enum class Prefetch { kNone, kEarly, kLate };
 template <int N>
 inline constexpr int kConvMinWavesPerEU = N <= 2048 ? 3 : 1;
 
-template <class IO, int N, bool kPerSignal, Prefetch kPf = Prefetch::kNone>
+// kDirect (per-signal filters, no prefetch): signal and filter load straight
+// into the first pass's registers and the output is stored from the last
+// pass's, with no LDS staging (DirectIO): 16384 x 2048 fp32 158 vs 164 us.
+template <class IO, int N, bool kPerSignal, Prefetch kPf = Prefetch::kNone, bool kDirect = false>
 __global__ __launch_bounds__(256) __attribute__((
     amdgpu_waves_per_eu(kPf != Prefetch::kNone ? 2 : kConvMinWavesPerEU<N>))) void
 conv1d_kernel(const IO* __restrict__ x, const IO* __restrict__ h, IO* __restrict__ y, int batch,
@@ -84,6 +87,17 @@ conv1d_kernel(const IO* __restrict__ x, const IO* __restrict__ h, IO* __restrict
                 fft_registers<N, true>(hs, io.slot, io.t, w);
             }
             io.stage(rx, v);
+        } else if constexpr (kPerSignal && kDirect) {
+            const DirectIO<IO, N> dio(threadIdx.x);
+            {
+                typename DirectIO<IO, N>::Raw rh;
+                dio.load(rh, h, tile, batch);
+                dio.decode(rh, hs);
+            }
+            typename DirectIO<IO, N>::Raw rx;
+            dio.load(rx, x, tile, batch);
+            fft_registers<N, true>(hs, io.slot, io.t, w);
+            dio.decode(rx, v);
         } else if constexpr (kPerSignal) {
             // The filter first, so its raw tile is dead before the signal's
             // arrives; float2 issues the signal's loads before transforming
@@ -113,7 +127,10 @@ conv1d_kernel(const IO* __restrict__ x, const IO* __restrict__ h, IO* __restrict
             v[j] = kPerSignal ? cmul(v[j], cpx{hs[j].re * kScale, hs[j].im * kScale})
                              : cmul(v[j], hs[j]);
         fft_registers<N, false>(v, io.slot, io.t, w);
-        io.store(v, y, tile, batch);
+        if constexpr (kDirect)
+            DirectIO<IO, N>(threadIdx.x).store(v, y, tile, batch);
+        else
+            io.store(v, y, tile, batch);
     }
 }
 

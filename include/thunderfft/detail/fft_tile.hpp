@@ -262,6 +262,43 @@ struct TileIO {
     }
 };
 
+// Direct movement between HBM and the first-pass layout, with no LDS
+// staging: lane t of transform f loads x[t + TPF*j] (j < 16) into its
+// registers, and stores y[t + TPF*j] from them.  One instruction of a wave
+// covers 64/TPF whole runs of TPF consecutive values (N >= 1024: 64
+// consecutive values of one transform), so every access is a full line.  A
+// transform past the end of the batch reads zeros and is not written.
+template <class IO, int N>
+struct DirectIO {
+    using P = C2CPlan<N>;
+    using W = typename Io<IO>::W1;
+    struct Raw {
+        W w[16];
+    };
+    int f, t;
+    __device__ __forceinline__ explicit DirectIO(int tid) : f(tid / P::kTPF), t(tid % P::kTPF) {}
+
+    __device__ __forceinline__ void load(Raw& r, const IO* __restrict__ base, long long tl,
+                                         long long batch) const {
+        const long long tr = tl * P::kFPB + f;
+        const W* p = reinterpret_cast<const W*>(base + tr * N + t);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) r.w[j] = tr < batch ? ld_nt(p + j * P::kTPF) : W{};
+    }
+    __device__ __forceinline__ static void decode(const Raw& r, cpx (&v)[16]) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = Io<IO>::decode1(r.w[j]);
+    }
+    __device__ __forceinline__ void store(const cpx (&v)[16], IO* __restrict__ base, long long tl,
+                                          long long batch) const {
+        const long long tr = tl * P::kFPB + f;
+        if (tr >= batch) return;
+        W* p = reinterpret_cast<W*>(base + tr * N + t);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) st_nt(p + j * P::kTPF, Io<IO>::encode1(v[j]));
+    }
+};
+
 // The tiles of workgroup blockIdx.x: first, first + step, ... while < end
 // (first >= end when it has none).
 //   tiles_per_block > 0: a contiguous run of that many (grids sized to the batch).

