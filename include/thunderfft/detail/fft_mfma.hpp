@@ -190,10 +190,11 @@ __device__ __forceinline__ void mfma_stage1_regs(const f16x8 (&a)[2],
 // registers); a transform of the other direction uses their conjugates.
 // On return lane (n = k1, q) holds, for block b = (f, m),
 // y[b][r] = X_f[k1 + 16 m + 16C (q + 4 r)].
-template <int C, bool FWD, bool TW_FWD = FWD>
-__device__ __forceinline__ void mfma_steps2to6(unsigned* region, const f16x8 (&a)[2],
-                                               const cpx* w1, const cpx* w2, int lane,
-                                               cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
+// `w1(c, r)` returns this lane's step-2 twiddle of block column c, output r.
+template <int C, bool FWD, bool TW_FWD = FWD, class W1>
+__device__ __forceinline__ void mfma_steps2to6_w(unsigned* region, const f16x8 (&a)[2], W1 w1,
+                                                 const cpx* w2, int lane,
+                                                 cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
     using P = MfmaPlan<C>;
     constexpr int kB = P::kBlocks;
     constexpr bool kConj = FWD != TW_FWD;
@@ -206,7 +207,7 @@ __device__ __forceinline__ void mfma_steps2to6(unsigned* region, const f16x8 (&a
             cpx v[C];
 #pragma unroll
             for (int c = 0; c < C; ++c) {
-                const cpx w = w1[(c * 4 + r) * 64 + lane];
+                const cpx w = w1(c, r);
                 v[c] = kConj ? cmulc(y[f * C + c][r], w) : cmul(y[f * C + c][r], w);
             }
             Dft<C, FWD>::run(v);
@@ -235,6 +236,15 @@ __device__ __forceinline__ void mfma_steps2to6(unsigned* region, const f16x8 (&a
     }
 }
 
+// Steps 2-6 with the step-2 twiddles in the workgroup's LDS table w1 = [c][r][lane].
+template <int C, bool FWD, bool TW_FWD = FWD>
+__device__ __forceinline__ void mfma_steps2to6(unsigned* region, const f16x8 (&a)[2],
+                                               const cpx* w1, const cpx* w2, int lane,
+                                               cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
+    mfma_steps2to6_w<C, FWD, TW_FWD>(
+        region, a, [&](int c, int r) { return w1[(c * 4 + r) * 64 + lane]; }, w2, lane, y);
+}
+
 // Steps 1-6 for the kFPW transforms a wave has staged in `region`.
 template <int C, bool FWD>
 __device__ __forceinline__ void mfma_fft_staged(unsigned* region, const f16x8 (&a)[2],
@@ -242,6 +252,41 @@ __device__ __forceinline__ void mfma_fft_staged(unsigned* region, const f16x8 (&
                                                 cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
     mfma_stage1_lds<C>(region, a, lane, y);
     mfma_steps2to6<C, FWD>(region, a, w1, w2, lane, y);
+}
+
+// One MFMA transform of the kFPW transforms a wave holds in registers, for
+// callers without the workgroup set-up (the device-side API): y[b][r] holds
+// z_f[16 c + n + 16C (q + 4 r)] for block b = (f, c) on entry (the layout the
+// transform leaves, so forward and inverse chain), and
+// X_f[k1 + 16 m + 16C (q + 4 r)] for block b = (f, m), k1 = n, on return.
+// Operands and twiddles are built from the positive-angle table `tw` of
+// length N for this call's direction; `region` is the wave's LDS scratch
+// (16 * kBlocks * 16 dwords), written after a wave-level sync.
+template <int C, bool FWD>
+__device__ __forceinline__ void mfma_fft_regs(unsigned* region, const float2* __restrict__ tw,
+                                              int lane, cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
+    constexpr int N = MfmaPlan<C>::N;
+    const int n = lane & 15, q = lane >> 4;
+    f16x8 a_in[2], a[2];
+    dft16_operands<FWD, true>(a_in, lane);
+    dft16_operands<FWD>(a, lane);
+    cpx w1[C * 4];
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float2 x = tw[((16 * c + n) * (q + 4 * r)) & (N - 1)];
+            w1[c * 4 + r] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+        }
+    cpx w2[C > 1 ? C - 1 : 1];
+#pragma unroll
+    for (int m = 1; m < C; ++m) {
+        const float2 x = tw[(16 * n * m) & (N - 1)];
+        w2[m - 1] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+    }
+    mfma_stage1_regs<C>(a_in, y);
+    mfma_steps2to6_w<C, FWD>(
+        region, a, [&](int c, int r) { return w1[c * 4 + r]; }, w2, lane, y);
 }
 
 // Batched C2C of half2 signals of N = 256*C on MFMA (C = 4 is N = 1024 as

@@ -115,7 +115,9 @@ struct LaneTwiddles {
     using P = C2CPlan<N>;
     PassTwiddles<N, P::kR1, 16> p1;
     PassTwiddles<N, (P::kR2 > 1 ? P::kR2 : 2), 16 * P::kR1> p2;  // unused when kR2 == 1
+    const float2* table = nullptr;  // the table itself (read by the device API's MFMA path)
     __device__ __forceinline__ void load(int t, const float2* __restrict__ tw) {
+        table = tw;
         p1.load(t, tw);
         if constexpr (P::kR2 > 1) p2.load(t, tw);
     }

@@ -11,12 +11,19 @@
 //  * A block is 256 lanes (any dim3 whose product is 256, e.g. 256 or
 //    (64, 4)), and processes batch_per_block<N> = 4096 / N transforms of
 //    length N.  Every lane holds 16 complex values ("the fragment").
-//  * Fragment order: lane tid belongs to transform f = tid / (N/16) and
-//    holds elements t + (N/16)*j, j = 0..15, of it, t = tid % (N/16).  The
-//    same order holds before and after ThunderFFT_kernel_reg, in both
-//    directions, so a forward transform, a pointwise product and an inverse
-//    transform chain in registers with no reordering (the reference needs a
-//    size-specific reorder between them).
+//  * Fragment order: register j of lane tid holds element
+//    fragment_element<T, N>(tid, j) of transform fragment_transform<T, N>(tid, j)
+//    of the block.  For float, and for half at N = 64, 128, 2048, 4096 (VALU
+//    transforms): transform tid / (N/16), element t + (N/16)*j,
+//    t = tid % (N/16).  For half at N = 256, 512, 1024 the transform runs on
+//    the matrix cores (v_mfma_f32_16x16x32_f16, as the library's own kernels)
+//    and the fragment is the MFMA layout: wave w = tid/64, lane n + 16q,
+//    j = 4b + r, transform w*(4/C) + b/C and element n + 16*(b%C) + 16C*(q+4r)
+//    with C = N/256.  Either way the same order holds before and after
+//    ThunderFFT_kernel_reg, in both directions, so a forward transform, a
+//    pointwise product and an inverse transform chain in registers with no
+//    reordering (the reference needs a size-specific reorder between them);
+//    the movement helpers below follow the order.
 //  * The workspace is caller-owned LDS of workspace_bytes<N, batch> bytes
 //    (8 bytes per complex value for both storage types: the FFT computes in
 //    fp32), 8-byte aligned.  All helpers are collective over the block, do
@@ -35,6 +42,7 @@
 
 #include <type_traits>
 
+#include "thunderfft/detail/fft_mfma.hpp"
 #include "thunderfft/detail/fft_tile.hpp"
 #include "thunderfft/thunderfft.hpp"
 
@@ -75,9 +83,51 @@ struct layout_t {
     }
 };
 
-// Per-lane twiddle factors of length N (a few registers; see fft_tile.hpp).
+// A bank-conflict-free shared-memory layout of the block's batch_per_block<N>
+// transforms for the fragment order of (T, N): ThunderFFT_smem2reg /
+// reg2smem through it read and write every LDS bank once per instruction.
+// VALU order: one pad value per 16 (as pad_h); MFMA order (C = N/256): 16 pad
+// values after every 16C, so the four lane groups q (16C apart) land on
+// different banks.
+template <typename T, int N>
+using fragment_layout = std::conditional_t<
+    std::is_same_v<T, half> && (N == 512 || N == 1024),
+    layout_t<N, batch_per_block<N>, 1, N, 16 * (N / 256), 16, false>,
+    std::conditional_t<std::is_same_v<T, half> && N == 256,
+                       layout_t<N, batch_per_block<N>, 1, N, 16, 0, false>,
+                       layout_t<N, batch_per_block<N>, 1, N, 16, 1, false>>>;
+
+// Per-lane twiddle factors of length N (a few registers; see fft_tile.hpp),
+// and the table they came from.
 template <int N>
 using lane_twiddles = thff::LaneTwiddles<N>;
+
+// True where half fragments use the MFMA layout (see the contract above).
+template <typename T, int N>
+inline constexpr bool fragment_on_mfma =
+    std::is_same_v<T, half> && (N == 256 || N == 512 || N == 1024);
+
+// Transform (of the block's batch_per_block<N>) and element index held by
+// register j of lane tid.
+template <typename T, int N>
+__device__ __forceinline__ int fragment_transform(int tid, int j) {
+    if constexpr (fragment_on_mfma<T, N>) {
+        constexpr int C = N / 256;
+        return (tid >> 6) * (4 / C) + (j >> 2) / C;
+    } else {
+        return tid / (N / 16);
+    }
+}
+template <typename T, int N>
+__device__ __forceinline__ int fragment_element(int tid, int j) {
+    if constexpr (fragment_on_mfma<T, N>) {
+        constexpr int C = N / 256;
+        const int lane = tid & 63;
+        return (lane & 15) + 16 * ((j >> 2) % C) + 16 * C * ((lane >> 4) + 4 * (j & 3));
+    } else {
+        return tid % (N / 16) + (N / 16) * j;
+    }
+}
 
 namespace detail {
 
@@ -128,15 +178,29 @@ template <typename T, int N, int batch, bool forward>
 __device__ __forceinline__ void ThunderFFT_kernel_reg(vec2_t<T>* __restrict__ reg,
                                                       const lane_twiddles<N>& W, void* workspace) {
     detail::check_shape<N, batch>();
-    using P = thff::C2CPlan<N>;
     const int tid = detail::block_tid();
-    thff::cpx* slot = static_cast<thff::cpx*>(workspace) + (tid / P::kTPF) * P::kSlot;
-    thff::cpx v[16];
+    if constexpr (fragment_on_mfma<T, N>) {
+        // The library's MFMA transform (thff::mfma_fft_regs): f16 data into
+        // each DFT16 stage, fp32 accumulation and twiddles; wave w uses 4 KiB
+        // of the workspace at w * 4 KiB.
+        constexpr int C = N / 256;
+        thff::cpx y[4][4];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = detail::to_cpx<T>(reg[j]);
-    thff::fft_registers<N, forward>(v, slot, tid % P::kTPF, W);
+        for (int j = 0; j < 16; ++j) y[j >> 2][j & 3] = detail::to_cpx<T>(reg[j]);
+        unsigned* region = static_cast<unsigned*>(workspace) + (tid >> 6) * 1024;
+        thff::mfma_fft_regs<C, forward>(region, W.table, tid & 63, y);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) reg[j] = detail::from_cpx<T>(v[j]);
+        for (int j = 0; j < 16; ++j) reg[j] = detail::from_cpx<T>(y[j >> 2][j & 3]);
+    } else {
+        using P = thff::C2CPlan<N>;
+        thff::cpx* slot = static_cast<thff::cpx*>(workspace) + (tid / P::kTPF) * P::kSlot;
+        thff::cpx v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = detail::to_cpx<T>(reg[j]);
+        thff::fft_registers<N, forward>(v, slot, tid % P::kTPF, W);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) reg[j] = detail::from_cpx<T>(v[j]);
+    }
 }
 
 // As above, loading the lane's twiddles from the device table W first.
@@ -155,11 +219,10 @@ template <typename T, int N, int batch>
 __device__ __forceinline__ void ThunderFFT_gmem2reg(vec2_t<T>* __restrict__ reg,
                                                     const vec2_t<T>* __restrict__ gmem) {
     detail::check_shape<N, batch>();
-    constexpr int TPF = N / 16;
     const int tid = detail::block_tid();
-    const vec2_t<T>* src = gmem + (tid / TPF) * N + tid % TPF;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) reg[j] = src[j * TPF];
+    for (int j = 0; j < 16; ++j)
+        reg[j] = gmem[fragment_transform<T, N>(tid, j) * N + fragment_element<T, N>(tid, j)];
 }
 
 // Fragment -> global memory, natural order (reference thunderfft.cuh:88-92).
@@ -167,11 +230,10 @@ template <typename T, int N, int batch>
 __device__ __forceinline__ void ThunderFFT_reg2gmem(vec2_t<T>* __restrict__ gmem,
                                                     const vec2_t<T>* __restrict__ reg) {
     detail::check_shape<N, batch>();
-    constexpr int TPF = N / 16;
     const int tid = detail::block_tid();
-    vec2_t<T>* dst = gmem + (tid / TPF) * N + tid % TPF;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) dst[j * TPF] = reg[j];
+    for (int j = 0; j < 16; ++j)
+        gmem[fragment_transform<T, N>(tid, j) * N + fragment_element<T, N>(tid, j)] = reg[j];
 }
 
 // Shared memory described by sL -> fragment (reference thunderfft.cuh:97-101).
@@ -179,11 +241,11 @@ template <typename T, typename sL>
 __device__ __forceinline__ void ThunderFFT_smem2reg(vec2_t<T>* __restrict__ reg,
                                                     const vec2_t<T>* __restrict__ smem) {
     detail::check_shape<sL::N, sL::batch>();
-    constexpr int TPF = sL::N / 16;
+    constexpr int N = sL::N;
     const int tid = detail::block_tid();
-    const int f = tid / TPF, t = tid % TPF;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) reg[j] = smem[sL::at(t + j * TPF, f)];
+    for (int j = 0; j < 16; ++j)
+        reg[j] = smem[sL::at(fragment_element<T, N>(tid, j), fragment_transform<T, N>(tid, j))];
 }
 
 // Fragment -> shared memory described by sL (reference thunderfft.cuh:106-110).
@@ -191,11 +253,11 @@ template <typename T, typename sL>
 __device__ __forceinline__ void ThunderFFT_reg2smem(vec2_t<T>* __restrict__ smem,
                                                     const vec2_t<T>* __restrict__ reg) {
     detail::check_shape<sL::N, sL::batch>();
-    constexpr int TPF = sL::N / 16;
+    constexpr int N = sL::N;
     const int tid = detail::block_tid();
-    const int f = tid / TPF, t = tid % TPF;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) smem[sL::at(t + j * TPF, f)] = reg[j];
+    for (int j = 0; j < 16; ++j)
+        smem[sL::at(fragment_element<T, N>(tid, j), fragment_transform<T, N>(tid, j))] = reg[j];
 }
 
 // Contiguous global tile -> shared memory described by sL (reference

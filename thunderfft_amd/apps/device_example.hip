@@ -72,10 +72,9 @@ __global__ __launch_bounds__(256) void fused_filter(const vec2_t<T>* in, vec2_t<
     thunderfft::ThunderFFT_load_twiddles<N>(w, tw);
     vec2_t<T> reg[thunderfft::elements_per_thread];
     thunderfft::ThunderFFT_gmem2reg<T, N, BPB>(reg, in + blockIdx.x * BPB * N);
-    // fp32 fragment for the product (the fragment holds bins t + (N/16) j)
+    // fp32 product; register j holds bin fragment_element<T, N>(tid, j)
     float2 spec[thunderfft::elements_per_thread];
     thunderfft::ThunderFFT_kernel_reg<T, N, BPB, true>(reg, w, work);
-    const int t = threadIdx.x % (N / 16);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
         float2 a;
@@ -83,7 +82,7 @@ __global__ __launch_bounds__(256) void fused_filter(const vec2_t<T>* in, vec2_t<
             a = reinterpret_cast<const float2&>(reg[j]);
         else
             a = __half22float2(reinterpret_cast<const __half2&>(reg[j]));
-        const float2 h = H[t + (N / 16) * j];
+        const float2 h = H[thunderfft::fragment_element<T, N>(threadIdx.x, j)];
         spec[j] = make_float2((a.x * h.x - a.y * h.y) / N, (a.x * h.y + a.y * h.x) / N);
         if constexpr (sizeof(vec2_t<T>) == 8)
             reinterpret_cast<float2&>(reg[j]) = spec[j];

@@ -82,8 +82,6 @@ __global__ void initialize(vec2_t<T>* input, double2* reference, size_t count, i
 
 // Natural-order staging layout with the library's padding (one slot of
 // N + N/16 values per transform).
-template <int N>
-using Staging = thunderfft::layout_t<N, thunderfft::batch_per_block<N>, 1, N, 16, 1, false>;
 
 template <class T, int N, bool kShared>
 __global__ __launch_bounds__(256) void repeat_kernel(const vec2_t<T>* __restrict__ in,
@@ -91,7 +89,7 @@ __global__ __launch_bounds__(256) void repeat_kernel(const vec2_t<T>* __restrict
                                                      const float2* __restrict__ table,
                                                      unsigned repeats) {
     constexpr int BPB = thunderfft::batch_per_block<N>;
-    using L = Staging<N>;
+    using L = thunderfft::fragment_layout<T, N>;
     __shared__ __align__(16) unsigned char work[thunderfft::workspace_bytes<N, BPB>];
     auto* staged = reinterpret_cast<vec2_t<T>*>(work);
     thunderfft::lane_twiddles<N> w;
