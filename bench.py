@@ -526,7 +526,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": load_traffic("float_fwd"),
-                     "kernel": "thff::c2c_kernel<float2,1024,true,false>",
+                     "kernel": "thff::c2c_kernel<float2, 1024, true, false, false>",
                      "algorithmic_bytes": main_run["bytes_per_call"]},
         "cpu_baseline": cpu,
         "also": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
