@@ -427,7 +427,12 @@ __global__ __launch_bounds__(256) void conv1d_real_filter_kernel(const float* __
     }
 }
 
-template <class IO, int N, Prefetch kPf = Prefetch::kNone>
+// kDirect (float, N >= 1024; used for N >= 2048): lane t of a transform loads samples
+// t + TPF*j of both rows straight into its first-pass registers (4-byte
+// accesses, 64 consecutive samples per wave instruction) and stores the
+// real and imaginary parts of its last-pass registers the same way, with no
+// LDS staging.
+template <class IO, int N, Prefetch kPf = Prefetch::kNone, bool kDirect = false>
 __global__ __launch_bounds__(256) void conv1d_real_kernel(
     const typename RealIo<IO>::S* __restrict__ x, const float2* __restrict__ spectrum,
     typename RealIo<IO>::S* __restrict__ y, int batch, int channels,
@@ -534,43 +539,82 @@ __global__ __launch_bounds__(256) void conv1d_real_kernel(
             rw.r1[i] = a1 >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + a1)) : u32x4{};
         }
     };
+    static_assert(!kDirect || (std::is_same_v<IO, float2> && N >= 1024),
+                  "direct real-conv movement: float, N >= 1024");
+    // Direct movement: this lane's 16 samples of both rows of transform f of
+    // tile tl (o0 / o1: offset of sample t of the row, -1: no such row).
+    struct DRows {
+        long long o0, o1;
+        float r0[16], r1[16];
+    };
+    auto dfetch = [&](long long tl, Pos q, DRows& rw) {
+        const long long tau = tl * P::kFPB + f;
+        long long pair;
+        int chan;
+        locate(q, f, pair, chan);
+        const long long b0 = 2 * pair, b1 = b0 + 1;
+        rw.o0 = tau < transforms ? (b0 * channels + chan) * N + t : -1;
+        rw.o1 = tau < transforms && b1 < batch ? (b1 * channels + chan) * N + t : -1;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            rw.r0[j] = rw.o0 >= 0 ? ld_nt(reinterpret_cast<const float*>(x) + rw.o0 + j * P::kTPF)
+                                  : 0.f;
+            rw.r1[j] = rw.o1 >= 0 ? ld_nt(reinterpret_cast<const float*>(x) + rw.o1 + j * P::kTPF)
+                                  : 0.f;
+        }
+    };
+    using RowsT = std::conditional_t<kDirect, DRows, Rows>;
+    auto fetch_any = [&](long long tl, Pos q, RowsT& rw) {
+        if constexpr (kDirect)
+            dfetch(tl, q, rw);
+        else
+            fetch(tl, q, rw);
+    };
     // The next tile's pieces load while the current tile is transformed
     // (kPf): early, right after the current tile's pieces are taken, or
     // late, after its product with the spectrum.
-    Rows next;
+    RowsT next;
     if constexpr (kPf != Prefetch::kNone)
-        if (tile < tile_end) fetch(tile, pos, next);
+        if (tile < tile_end) fetch_any(tile, pos, next);
 
     for (; tile < tile_end; tile += step) {
-        // ---- both rows of each transform -> LDS as (re, im) = (row 0, row 1) ----
-        Rows cur;
+        // ---- both rows of each transform -> (re, im) = (row 0, row 1) ----
+        RowsT cur;
         const Pos at = pos;
         pos = advance(pos);
         if constexpr (kPf == Prefetch::kEarly) {
             cur = next;
-            if (tile + step < tile_end) fetch(tile + step, pos, next);
+            if (tile + step < tile_end) fetch_any(tile + step, pos, next);
         } else if constexpr (kPf == Prefetch::kLate) {
+            if constexpr (kDirect) {
+                cur.o0 = next.o0, cur.o1 = next.o1;
+            } else {
 #pragma unroll
-            for (int i = 0; i < kRowOffsets; ++i) cur.o0[i] = next.o0[i], cur.o1[i] = next.o1[i];
+                for (int i = 0; i < kRowOffsets; ++i) cur.o0[i] = next.o0[i], cur.o1[i] = next.o1[i];
+            }
         } else {
-            fetch(tile, at, cur);
+            fetch_any(tile, at, cur);
         }
-        const u32x4* r0 = kPf == Prefetch::kLate ? next.r0 : cur.r0;
-        const u32x4* r1 = kPf == Prefetch::kLate ? next.r1 : cur.r1;
-        region_sync<P::kWaveLocal>();
-#pragma unroll
-        for (int i = 0; i < kSteps; ++i) {
-            const int e = 1024 * wave + kVec * lane + 64 * kVec * i;
-            float a[kVec], b[kVec];
-            R::decode(r0[i], a);
-            R::decode(r1[i], b);
-#pragma unroll
-            for (int c = 0; c < kVec; ++c) lds[lds_pad(e + c)] = cpx{a[c], b[c]};
-        }
-        region_sync<P::kWaveLocal>();
+        const RowsT& src = kPf == Prefetch::kLate ? next : cur;
         cpx v[16];
+        if constexpr (kDirect) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = slot[lds_pad(t + j * P::kTPF)];
+            for (int j = 0; j < 16; ++j) v[j] = cpx{src.r0[j], src.r1[j]};
+        } else {
+            region_sync<P::kWaveLocal>();
+#pragma unroll
+            for (int i = 0; i < kSteps; ++i) {
+                const int e = 1024 * wave + kVec * lane + 64 * kVec * i;
+                float a[kVec], b[kVec];
+                R::decode(src.r0[i], a);
+                R::decode(src.r1[i], b);
+#pragma unroll
+                for (int c = 0; c < kVec; ++c) lds[lds_pad(e + c)] = cpx{a[c], b[c]};
+            }
+            region_sync<P::kWaveLocal>();
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = slot[lds_pad(t + j * P::kTPF)];
+        }
 
         // ---- FFT, product with the channel's spectrum, inverse FFT ----
         // (a channel past the last transform too: always a valid spectrum row)
@@ -599,26 +643,35 @@ __global__ __launch_bounds__(256) void conv1d_real_kernel(
             }
         }
         if constexpr (kPf == Prefetch::kLate)
-            if (tile + step < tile_end) fetch(tile + step, pos, next);
+            if (tile + step < tile_end) fetch_any(tile + step, pos, next);
         fft_registers<N, false>(v, slot, t, w);
 
         // ---- real part -> row 0, imaginary part -> row 1 ----
-        region_sync<P::kWaveLocal>();
+        if constexpr (kDirect) {
+            float* yf = reinterpret_cast<float*>(y);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) slot[lds_pad(t + j * P::kTPF)] = v[j];
-        region_sync<P::kWaveLocal>();
-#pragma unroll
-        for (int i = 0; i < kSteps; ++i) {
-            const int e = 1024 * wave + kVec * lane + 64 * kVec * i;
-            float a[kVec], b[kVec];
-#pragma unroll
-            for (int c = 0; c < kVec; ++c) {
-                const cpx z = lds[lds_pad(e + c)];
-                a[c] = z.re, b[c] = z.im;
+            for (int j = 0; j < 16; ++j) {
+                if (cur.o0 >= 0) st_nt(yf + cur.o0 + j * P::kTPF, v[j].re);
+                if (cur.o1 >= 0) st_nt(yf + cur.o1 + j * P::kTPF, v[j].im);
             }
-            const long long a0 = piece(cur.o0, i), a1 = piece(cur.o1, i);
-            if (a0 >= 0) st_nt(reinterpret_cast<u32x4*>(y + a0), R::encode(a));
-            if (a1 >= 0) st_nt(reinterpret_cast<u32x4*>(y + a1), R::encode(b));
+        } else {
+            region_sync<P::kWaveLocal>();
+#pragma unroll
+            for (int j = 0; j < 16; ++j) slot[lds_pad(t + j * P::kTPF)] = v[j];
+            region_sync<P::kWaveLocal>();
+#pragma unroll
+            for (int i = 0; i < kSteps; ++i) {
+                const int e = 1024 * wave + kVec * lane + 64 * kVec * i;
+                float a[kVec], b[kVec];
+#pragma unroll
+                for (int c = 0; c < kVec; ++c) {
+                    const cpx z = lds[lds_pad(e + c)];
+                    a[c] = z.re, b[c] = z.im;
+                }
+                const long long a0 = piece(cur.o0, i), a1 = piece(cur.o1, i);
+                if (a0 >= 0) st_nt(reinterpret_cast<u32x4*>(y + a0), R::encode(a));
+                if (a1 >= 0) st_nt(reinterpret_cast<u32x4*>(y + a1), R::encode(b));
+            }
         }
     }
 }

@@ -287,8 +287,11 @@ hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectr
     const ConvShape shape = valu_conv_shape<N>(precision, true, false);
     const Grid g = make_grid(ntiles, shape.per_cu, num_cus);
     constexpr Prefetch kF32 = valu_conv_shape<N>(0, true, false).prefetch;
+    // fp32 N >= 2048 moves samples straight between HBM and registers
+    // (conv1d_real_kernel's kDirect): N = 4096 108-114 us against 115-117,
+    // 2048 115-119 against 120-123; at N = 1024 it measured slower (125 vs 113).
     if (precision == 0)
-        conv1d_real_kernel<float2, N, kF32><<<g.blocks, 256, 0, stream>>>(
+        conv1d_real_kernel<float2, N, kF32, (N >= 2048)><<<g.blocks, 256, 0, stream>>>(
             static_cast<const float*>(x), spectrum, static_cast<float*>(y), batch, channels, tw,
             g.tiles_per_block);
     else
