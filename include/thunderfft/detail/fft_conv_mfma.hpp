@@ -303,13 +303,7 @@ namespace thff {
 //            exchange with t0' = 4 w + b, t1' = n, stage 2, transpose,
 //            stage 3 -> y[k1' + 16 k2' + 256 k3'], then staged output split
 //            back into the two rows.
-// Exchange element (k1, t0, t1) sits at 272 k1 + 16 t0 + 4 (((t1 >> 2) +
-// (t0 >> 2)) & 3) + ((t1 + k1) & 3); for the inverse's writers (fixed b, r)
-// the banks are 16 (b + q) + 4 (((n >> 2) + w) & 3) + (((n & 3) + q) & 3)
-// mod 64, all different, as for the forward ones.
-__device__ __forceinline__ int xaddr4096(int k1, int t0, int t1) {
-    return Mfma4096::kMatrix * k1 + 16 * t0 + 4 * (((t1 >> 2) + (t0 >> 2)) & 3) + ((t1 + k1) & 3);
-}
+// The exchange layout is xaddr4096 (fft_mfma.hpp).
 
 template <int N>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void

@@ -418,6 +418,79 @@ struct Mfma4096 {
     __device__ static __forceinline__ int out_pad(int k) { return k + (k >> 6); }
 };
 
+// Exchange element (k1, t0, t1) sits at 272 k1 + 16 t0 + 4 (((t1 >> 2) +
+// (t0 >> 2)) & 3) + ((t1 + k1) & 3); for the inverse's writers (fixed b, r)
+// the banks are 16 (b + q) + 4 (((n >> 2) + w) & 3) + (((n & 3) + q) & 3)
+// mod 64, all different, as for the forward ones.
+__device__ __forceinline__ int xaddr4096(int k1, int t0, int t1) {
+    return Mfma4096::kMatrix * k1 + 16 * t0 + 4 * (((t1 >> 2) + (t0 >> 2)) & 3) + ((t1 + k1) & 3);
+}
+
+// One N = 4096 transform per workgroup from registers, either direction, for
+// callers without the kernel's set-up (the device-side API).  Lane (n, q) of
+// wave w holds, in v[b][r], element 4 w + b + 16 n + 256 (q + 4 r) on entry
+// and on return (the layout the three stages leave, so transforms chain):
+// stage 1 over k3 = q + 4 r for the sequences t' = 4 w + b + 16 n
+// (column-permuted operands), W^(t' k1), the workgroup exchange with
+// t0 = 4 w + b, t1 = n, stage 2, W_256^(t0 k2), the wave-local transpose
+// and stage 3.  xbuf: Mfma4096::kExchange dwords of LDS; two workgroup
+// barriers, the first before xbuf is written.  Operands and twiddles come
+// from the positive-angle table `tw` of length 4096.
+template <bool FWD>
+__device__ __forceinline__ void mfma4096_fft_regs(unsigned* xbuf, const float2* __restrict__ tw,
+                                                  int tid, cpx (&v)[4][4]) {
+    using P = Mfma4096;
+    constexpr int N = P::N;
+    const int wave = tid >> 6, lane = tid & 63, n = lane & 15, q = lane >> 4;
+    unsigned* const region = xbuf + 4 * P::kMatrix * wave;
+    f16x8 a[2], a_in[2];
+    dft16_operands<FWD>(a, lane);
+    dft16_operands<FWD, true>(a_in, lane);
+    auto tw_at = [&](int k) {
+        const float2 x = tw[k & (N - 1)];
+        return FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+    };
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        u32x4 xv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xv[r] = pack_half2(v[b][r]);
+        dft16_block(a_in, as_f16x8(xv), v[b]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], tw_at((4 * wave + b + 16 * n) * (q + 4 * r)));
+    }
+    __syncthreads();  // every wave is done with xbuf
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xbuf[xaddr4096(q + 4 * r, 4 * wave + b, n)] = pack_half2(v[b][r]);
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const u32x4 raw = *reinterpret_cast<const u32x4*>(
+            region + P::kMatrix * b + 16 * n + 4 * ((q + (n >> 2)) & 3));
+        u32x4 xv;  // t1 = 4 q + e sits at position (e + k1) & 3 = (e + b) & 3
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[e] = raw[(e + b) & 3];
+        dft16_block(a, as_f16x8(xv), v[b]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], tw_at(16 * n * (q + 4 * r)));
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            region[(16 * b + q + 4 * r) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] = pack_half2(v[b][r]);
+    wave_lds_sync();
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(
+            region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+        dft16_block(a, as_f16x8(xv), v[b]);
+    }
+}
+
 template <bool FWD, bool kPrefetch>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c2c_mfma4096_kernel(
     const __half2* __restrict__ in, __half2* __restrict__ out, int batch,

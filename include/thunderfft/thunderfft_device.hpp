@@ -13,13 +13,14 @@
 //    length N.  Every lane holds 16 complex values ("the fragment").
 //  * Fragment order: register j of lane tid holds element
 //    fragment_element<T, N>(tid, j) of transform fragment_transform<T, N>(tid, j)
-//    of the block.  For float, and for half at N = 64, 128, 2048, 4096 (VALU
+//    of the block.  For float, and for half at N = 64, 128, 2048 (VALU
 //    transforms): transform tid / (N/16), element t + (N/16)*j,
-//    t = tid % (N/16).  For half at N = 256, 512, 1024 the transform runs on
-//    the matrix cores (v_mfma_f32_16x16x32_f16, as the library's own kernels)
-//    and the fragment is the MFMA layout: wave w = tid/64, lane n + 16q,
-//    j = 4b + r, transform w*(4/C) + b/C and element n + 16*(b%C) + 16C*(q+4r)
-//    with C = N/256.  Either way the same order holds before and after
+//    t = tid % (N/16).  For half at N = 256, 512, 1024, 4096 the transform
+//    runs on the matrix cores (v_mfma_f32_16x16x32_f16, as the library's own
+//    kernels) and the fragment is the MFMA layout: wave w = tid/64, lane
+//    n + 16q, j = 4b + r; N = 256C (C = 1, 2, 4): transform w*(4/C) + b/C,
+//    element n + 16*(b%C) + 16C*(q+4r); N = 4096: element
+//    4w + b + 16n + 256*(q+4r).  Either way the same order holds before and after
 //    ThunderFFT_kernel_reg, in both directions, so a forward transform, a
 //    pointwise product and an inverse transform chain in registers with no
 //    reordering (the reference needs a size-specific reorder between them);
@@ -91,11 +92,14 @@ struct layout_t {
 // different banks.
 template <typename T, int N>
 using fragment_layout = std::conditional_t<
+    std::is_same_v<T, half> && N == 4096,
+    layout_t<N, batch_per_block<N>, 1, N, 64, 1, false>,
+    std::conditional_t<
     std::is_same_v<T, half> && (N == 512 || N == 1024),
     layout_t<N, batch_per_block<N>, 1, N, 16 * (N / 256), 16, false>,
     std::conditional_t<std::is_same_v<T, half> && N == 256,
                        layout_t<N, batch_per_block<N>, 1, N, 16, 0, false>,
-                       layout_t<N, batch_per_block<N>, 1, N, 16, 1, false>>>;
+                       layout_t<N, batch_per_block<N>, 1, N, 16, 1, false>>>>;
 
 // Per-lane twiddle factors of length N (a few registers; see fft_tile.hpp),
 // and the table they came from.
@@ -105,13 +109,15 @@ using lane_twiddles = thff::LaneTwiddles<N>;
 // True where half fragments use the MFMA layout (see the contract above).
 template <typename T, int N>
 inline constexpr bool fragment_on_mfma =
-    std::is_same_v<T, half> && (N == 256 || N == 512 || N == 1024);
+    std::is_same_v<T, half> && (N == 256 || N == 512 || N == 1024 || N == 4096);
 
 // Transform (of the block's batch_per_block<N>) and element index held by
 // register j of lane tid.
 template <typename T, int N>
 __device__ __forceinline__ int fragment_transform(int tid, int j) {
-    if constexpr (fragment_on_mfma<T, N>) {
+    if constexpr (fragment_on_mfma<T, N> && N == 4096) {
+        return 0;
+    } else if constexpr (fragment_on_mfma<T, N>) {
         constexpr int C = N / 256;
         return (tid >> 6) * (4 / C) + (j >> 2) / C;
     } else {
@@ -120,7 +126,10 @@ __device__ __forceinline__ int fragment_transform(int tid, int j) {
 }
 template <typename T, int N>
 __device__ __forceinline__ int fragment_element(int tid, int j) {
-    if constexpr (fragment_on_mfma<T, N>) {
+    if constexpr (fragment_on_mfma<T, N> && N == 4096) {
+        const int lane = tid & 63;
+        return 4 * (tid >> 6) + (j >> 2) + 16 * (lane & 15) + 256 * ((lane >> 4) + 4 * (j & 3));
+    } else if constexpr (fragment_on_mfma<T, N>) {
         constexpr int C = N / 256;
         const int lane = tid & 63;
         return (lane & 15) + 16 * ((j >> 2) % C) + 16 * C * ((lane >> 4) + 4 * (j & 3));
@@ -179,7 +188,16 @@ __device__ __forceinline__ void ThunderFFT_kernel_reg(vec2_t<T>* __restrict__ re
                                                       const lane_twiddles<N>& W, void* workspace) {
     detail::check_shape<N, batch>();
     const int tid = detail::block_tid();
-    if constexpr (fragment_on_mfma<T, N>) {
+    if constexpr (fragment_on_mfma<T, N> && N == 4096) {
+        // The library's three-stage MFMA transform (thff::mfma4096_fft_regs);
+        // 17 KiB of the workspace; two workgroup barriers.
+        thff::cpx y[4][4];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) y[j >> 2][j & 3] = detail::to_cpx<T>(reg[j]);
+        thff::mfma4096_fft_regs<forward>(static_cast<unsigned*>(workspace), W.table, tid, y);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) reg[j] = detail::from_cpx<T>(y[j >> 2][j & 3]);
+    } else if constexpr (fragment_on_mfma<T, N>) {
         // The library's MFMA transform (thff::mfma_fft_regs): f16 data into
         // each DFT16 stage, fp32 accumulation and twiddles; wave w uses 4 KiB
         // of the workspace at w * 4 KiB.
