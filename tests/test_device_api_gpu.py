@@ -47,6 +47,7 @@ def ex():
     L.thffx_device_fft.argtypes = [ci, ci, ci, vp, vp, ci, vp, vp]
     L.thffx_device_fft_reg.argtypes = [ci, ci, ci, vp, vp, ci, vp]
     L.thffx_fused_filter.argtypes = [ci, ci, vp, vp, vp, ci, vp]
+    L.thffx_fragment_map.argtypes = [ci, ci, vp, vp]
     yield L
     thff.ThunderFFTFinalize("float")
     thff.ThunderFFTFinalize("half")
@@ -115,3 +116,23 @@ def test_device_api_fused_filter(ex, T, n):
     # half: the spectrum is also rounded to binary16 between the transforms
     assert m["nonfinite"] == 0 and m["rel_l2"] <= GATE
     assert m["rel_l2"] <= (5e-6 if T == "float" else 2e-3), label
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+def test_fragment_order_is_a_bijection(ex, T):
+    """fragment_transform / fragment_element map the block's 256 lanes x 16
+    registers one-to-one onto its batch_per_block<N> transforms x N elements, for
+    every length (half at N = 256, 512, 1024, 4096 uses the MFMA layouts)."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    for n in SIZES:
+        d_map = torch.full((2 * 256 * 16,), -1, dtype=torch.int32, device="cuda")
+        assert ex.thffx_fragment_map(PREC[T], n, d_map.data_ptr(), None) == 0
+        m = d_map.cpu().numpy().reshape(256 * 16, 2)
+        bpb = thff.transforms_per_block(n)
+        assert m[:, 0].min() >= 0 and m[:, 0].max() < bpb, (T, n)
+        assert m[:, 1].min() >= 0 and m[:, 1].max() < n, (T, n)
+        flat = m[:, 0].astype(np.int64) * n + m[:, 1]
+        assert np.unique(flat).size == bpb * n == 4096, (T, n)

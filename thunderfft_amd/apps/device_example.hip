@@ -94,6 +94,33 @@ __global__ __launch_bounds__(256) void fused_filter(const vec2_t<T>* in, vec2_t<
     thunderfft::ThunderFFT_reg2gmem<T, N, BPB>(out + blockIdx.x * BPB * N, reg);
 }
 
+// (transform, element) of every (lane, register) of one block:
+// map[2 * (16 * tid + j)] = fragment_transform, [... + 1] = fragment_element.
+template <class T, int N>
+__global__ __launch_bounds__(256) void fragment_map(int* map) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < thunderfft::elements_per_thread; ++j) {
+        map[2 * (16 * tid + j)] = thunderfft::fragment_transform<T, N>(tid, j);
+        map[2 * (16 * tid + j) + 1] = thunderfft::fragment_element<T, N>(tid, j);
+    }
+}
+
+template <class T>
+int launch_map(int n, int* map, hipStream_t s) {
+    switch (n) {
+    case 64: fragment_map<T, 64><<<1, 256, 0, s>>>(map); break;
+    case 128: fragment_map<T, 128><<<1, 256, 0, s>>>(map); break;
+    case 256: fragment_map<T, 256><<<1, 256, 0, s>>>(map); break;
+    case 512: fragment_map<T, 512><<<1, 256, 0, s>>>(map); break;
+    case 1024: fragment_map<T, 1024><<<1, 256, 0, s>>>(map); break;
+    case 2048: fragment_map<T, 2048><<<1, 256, 0, s>>>(map); break;
+    case 4096: fragment_map<T, 4096><<<1, 256, 0, s>>>(map); break;
+    default: return -22;
+    }
+    return hipGetLastError() == hipSuccess && hipStreamSynchronize(s) == hipSuccess ? 0 : -5;
+}
+
 template <class T, int N>
 int launch(int kind, int forward, const void* x, void* y, const void* H, int batch,
            const float2* tw, int* guard, hipStream_t s) {
@@ -144,6 +171,13 @@ int run(int precision, int n, int kind, int forward, const void* x, void* y, con
 }  // namespace
 
 extern "C" {
+// 2 * 256 * 16 ints: the fragment order of (precision, n) for one block.
+int thffx_fragment_map(int precision, int n, int* d_map, void* stream) {
+    if (!d_map) return -22;
+    auto s = static_cast<hipStream_t>(stream);
+    return precision == THFF_FLOAT ? launch_map<float>(n, d_map, s) : launch_map<half>(n, d_map, s);
+}
+
 int thffx_device_fft(int precision, int n, int forward, const void* x, void* y, int batch,
                      int* d_guard_changes, void* stream) {
     return run(precision, n, 0, forward, x, y, nullptr, batch, d_guard_changes, stream);
