@@ -195,6 +195,14 @@ int thff_twiddle_info(int precision, const void** d_table, int* n);
 int thff_fill_uniform(int precision, void* d_out, long long count, unsigned long long seed,
                       long long first_element, void* stream);
 
+/* Benchmark helper (no reference counterpart): copies `bytes` (a multiple
+ * of 16) from d_src to d_dst with one 16-byte non-temporal load and store per
+ * lane, the fastest streaming copy measured on MI355X.  It gives the device's
+ * read-plus-write ceiling beside the transforms (bench.py).  Null,
+ * misaligned or overlapping buffers and bad sizes -> THFF_EINVAL before any
+ * HIP call; bytes = 0 is a no-op.  Asynchronous on `stream`. */
+int thff_copy_nt(void* d_dst, const void* d_src, long long bytes, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

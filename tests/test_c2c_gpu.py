@@ -296,3 +296,20 @@ def test_thff_validate_matrix(mode, tmp_path):
         worst[k] = max(worst.get(k, 0.0), float(r["relative_l2"]))
     print("worst relative L2 per precision:", worst, flush=True)
     assert worst["fp32"] <= TIGHT["float"] and worst["fp16"] <= TIGHT["half"]
+
+
+def test_copy_nt_copies_every_byte():
+    """thff_copy_nt (the bandwidth reference bench.py reports) moves exactly the
+    requested bytes: whole 8 KiB blocks plus a tail, nothing past the end."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    for nbytes in (16, 8192, 16 * (512 * 37 + 13)):
+        src = torch.randint(-2**31, 2**31 - 1, (nbytes // 4 + 8,), dtype=torch.int32, device="cuda")
+        dst = torch.full_like(src, 0x5A5A5A5A)
+        thff.copy_nt(dst, src, nbytes)
+        torch.cuda.synchronize()
+        k = nbytes // 4
+        assert torch.equal(dst[:k], src[:k]), nbytes
+        assert bool((dst[k:] == 0x5A5A5A5A).all()), nbytes

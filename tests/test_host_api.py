@@ -172,3 +172,14 @@ def test_misaligned_buffers_rejected():
             thff.ThunderFFT_conv1d(T, 64, 16, 32, 56, 1, False)
         with pytest.raises(ValueError, match="16-byte aligned"):
             thff.ThunderFFT_conv2d(T, 64, 64, 24, 32, 48, 1)
+
+
+def test_copy_nt_argument_checks():
+    """The benchmark's streaming copy rejects bad sizes and null, misaligned or
+    overlapping buffers (THFF_EINVAL, before any HIP call); zero bytes is a no-op."""
+    thff.copy_nt(0, 0, 0)
+    for dst, src, n in ((4096, 0, 16), (0, 4096, 16), (4104, 8192, 16), (4096, 8200, 32),
+                        (4096, 8192, 24), (4096, 8192, -16), (4096, 4096 + 16, 64),
+                        (4096 + 16, 4096, 64)):
+        with pytest.raises(ValueError):
+            thff.copy_nt(dst, src, n)

@@ -25,7 +25,7 @@ __all__ = [
     "SUPPORTED_N", "PRECISIONS", "lib", "ThunderFFTInitialize", "ThunderFFTFinalize",
     "ThunderFFT_global", "ThunderFFT_global_async", "twiddle_info", "fill_uniform",
     "fft", "transforms_per_block", "LIB_PATH", "ThunderFFT_conv1d", "ThunderFFT_conv1d_async",
-    "ThunderFFT_conv2d", "ThunderFFT_conv2d_async",
+    "ThunderFFT_conv2d", "ThunderFFT_conv2d_async", "copy_nt",
 ]
 
 SUPPORTED_N = (64, 128, 256, 512, 1024, 2048, 4096)
@@ -80,6 +80,7 @@ def lib() -> ctypes.CDLL:
                                         ctypes.POINTER(ctypes.c_int)]
         L.thff_fill_uniform.argtypes = [ctypes.c_int, vp, ctypes.c_longlong, ctypes.c_ulonglong,
                                         ctypes.c_longlong, vp]
+        L.thff_copy_nt.argtypes = [vp, vp, ctypes.c_longlong, vp]
         _lib = L
     return _lib
 
@@ -232,6 +233,11 @@ def fill_uniform(T, d_out, count: int, seed: int, first_element: int = 0, stream
     """Seeded U[-1,1) complex values (same formula as the test oracle's generator)."""
     _raise(lib().thff_fill_uniform(_precision(T), _ptr(d_out), int(count),
                                    int(seed) & (2**64 - 1), int(first_element), _stream(stream)))
+
+
+def copy_nt(d_dst, d_src, nbytes: int, stream=0) -> None:
+    """Non-temporal 16-byte streaming copy (the bandwidth ceiling bench.py reports)."""
+    _raise(lib().thff_copy_nt(_ptr(d_dst), _ptr(d_src), int(nbytes), _stream(stream)))
 
 
 def transforms_per_block(N: int) -> int:

@@ -503,4 +503,19 @@ int thff_fill_uniform(int precision, void* d_out, long long count, unsigned long
     return THFF_OK;
 }
 
+int thff_copy_nt(void* d_dst, const void* d_src, long long bytes, void* stream) {
+    if (bytes < 0 || bytes % 16 != 0)
+        return fail(THFF_EINVAL, "thff_copy_nt: bytes must be a non-negative multiple of 16");
+    if (bytes == 0) return THFF_OK;
+    if (!d_dst || !d_src) return fail(THFF_EINVAL, "thff_copy_nt: null pointer");
+    const auto d = reinterpret_cast<unsigned long long>(d_dst);
+    const auto s = reinterpret_cast<unsigned long long>(d_src);
+    if ((d | s) & 15) return fail(THFF_EINVAL, "thff_copy_nt: buffers must be 16-byte aligned");
+    const auto ub = static_cast<unsigned long long>(bytes);
+    if (d < s + ub && s < d + ub) return fail(THFF_EINVAL, "thff_copy_nt: buffers overlap");
+    const hipError_t err = thff::launch_copy_nt(d_dst, d_src, bytes, static_cast<hipStream_t>(stream));
+    if (err != hipSuccess) return fail_hip(err, "thff_copy_nt launch");
+    return THFF_OK;
+}
+
 }  // extern "C"

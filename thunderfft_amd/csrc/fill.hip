@@ -38,7 +38,28 @@ __global__ __launch_bounds__(256) void fill_uniform_kernel(IO* out, long long co
     }
 }
 
+// Streaming copy: one 16-byte vector per lane, non-temporal load and store.
+// Of 1, 2, 4 and 8 vectors per lane (all loads before all stores), one
+// streams best on MI355X: 512 MiB each way at 6.60 TB/s against 6.20, 6.11
+// and 5.85 TB/s.
+using u32x4v = unsigned __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void copy_nt_kernel(const u32x4v* __restrict__ src,
+                                                      u32x4v* __restrict__ dst, long long n16) {
+    const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n16) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
 }  // namespace
+
+hipError_t launch_copy_nt(void* dst, const void* src, long long bytes, hipStream_t stream) {
+    const long long n16 = bytes / 16;
+    if (n16 <= 0) return hipSuccess;
+    const long long blocks = (n16 + 255) / 256;
+    if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+    copy_nt_kernel<<<static_cast<unsigned>(blocks), 256, 0, stream>>>(
+        static_cast<const u32x4v*>(src), static_cast<u32x4v*>(dst), n16);
+    return hipGetLastError();
+}
 
 hipError_t launch_fill_uniform(int precision, void* out, long long count, unsigned long long seed,
                                long long first_element, hipStream_t stream) {

@@ -50,5 +50,6 @@ int c2c_transforms_per_block(int n);
 
 hipError_t launch_fill_uniform(int precision, void* out, long long count, unsigned long long seed,
                                long long first_element, hipStream_t stream);
+hipError_t launch_copy_nt(void* dst, const void* src, long long bytes, hipStream_t stream);
 
 }  // namespace thff
