@@ -232,7 +232,7 @@ __device__ __forceinline__ void forward(cpx (&v)[16], cpx* lds, int tid, const T
 #pragma unroll
     for (int r0 = 0; r0 < 4; ++r0)
 #pragma unroll
-        for (int c0_ = 1; c0_ < 4; ++c0_) v[4 * r0 + c0_] = twiddle<true>(v[4 * r0 + c0_], w.wc[c0_ - 1]);
+        for (int c = 1; c < 4; ++c) v[4 * r0 + c] = twiddle<true>(v[4 * r0 + c], w.wc[c - 1]);
     dft4s<true, 1, 4>(v);  // over c0
 #pragma unroll
     for (int r0 = 1; r0 < 4; ++r0)
@@ -254,7 +254,7 @@ __device__ __forceinline__ void inverse(cpx (&v)[16], cpx* lds, int tid, const T
 #pragma unroll
     for (int r0 = 0; r0 < 4; ++r0)
 #pragma unroll
-        for (int c0_ = 1; c0_ < 4; ++c0_) v[4 * r0 + c0_] = twiddle<false>(v[4 * r0 + c0_], w.wc[c0_ - 1]);
+        for (int c = 1; c < 4; ++c) v[4 * r0 + c] = twiddle<false>(v[4 * r0 + c], w.wc[c - 1]);
     __syncthreads();  // every wave is done with its E2 reads
     cpx* q = lds + 17 * (tid >> 4) + (tid & 15);
 #pragma unroll
