@@ -38,7 +38,11 @@ inline Grid make_grid(long long ntiles, int per_cu, int num_cus) {
 // transformed.  Measured at batch = 2^26/N:
 //   fp32 N <= 1024: one tile per workgroup, 172-177 us (device grids: 181+).
 //   fp32 N = 2048, 4096: 16 per CU with prefetch, 184 us (one or two tiles
-//     per workgroup: 188-194 us).
+//     per workgroup: 188-194 us); with direct movement, same box: 178 / 180 us
+//     against 12 per CU 181 / 179, 8 per CU 184 / 180, 4 per CU 189 / 181,
+//     8 per CU without prefetch 186 / 186, one tile per workgroup 181 / 186.
+//   fp16 N = 2048 (MFMA): 2 per CU 93-94 us against 1 per CU 111 (with
+//     prefetch 95), 3 per CU 106, one tile per workgroup 122.
 //   fp16 N = 64, 128 (VALU): one tile per workgroup.
 //   fp16 MFMA: 2 per CU, 87-94 us (two tiles per workgroup: 87-98 us; N = 4096
 //     with contiguous shares: 99 us); N = 2048 without prefetch, which would
