@@ -710,7 +710,10 @@ inline constexpr bool kValidPrefetch = std::is_same_v<IO, float2>;
 template <class IO>
 inline constexpr int kValidMinWavesPerEU = kValidPrefetch<IO> ? 2 : 3;
 
-template <class IO>
+// kExact: the 64-point passes use exact per-lane twiddles (LaneTwiddles64Exact,
+// 610 instead of 666 VALU instructions per window group, 243 VGPRs): float2
+// only, which already runs at 2 waves per SIMD; 227 vs 233 us at 2^26 values.
+template <class IO, bool kExact = kValidPrefetch<IO>>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kValidMinWavesPerEU<IO>))) void conv1d_valid_kernel(
     const IO* __restrict__ x, const float2* __restrict__ taps, IO* __restrict__ y,
     long long len, int ntaps, int batch, const float2* __restrict__ tw, int groups_per_block) {
@@ -729,7 +732,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kValidMinWa
     cpx* const region = lds + wave * kWindowsPerWave * P::kSlot;  // 16 slots = 1088 >= kSpan
     cpx* const slot = region + fl * P::kSlot;
 
-    LaneTwiddles<64> w;
+    std::conditional_t<kExact, LaneTwiddles64Exact, LaneTwiddles<64>> w;
     w.load(t, tw);
 
     const int V = 65 - ntaps;                            // valid outputs per window
