@@ -33,6 +33,7 @@ import json
 import math
 import os
 import re
+import statistics
 import sys
 import time
 
@@ -50,6 +51,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-fp64-check", action="store_true",
+                    help="skip the timed host fp64 check of the GPU output")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target wall time of the CPU baseline sample")
     ap.add_argument("--prewarm-ms", type=float, default=250.0,
@@ -67,9 +70,16 @@ def parse():
 SETTLE_MS = 60.0  # set from --settle-ms in main()
 
 
+PER_LAUNCH = 25  # individually timed launches per leg (their median is reported)
+LAST_MEDIAN_MS = None  # median of the last leg's per-launch timings, set by timed()
+
+
 def timed(launch, steps: int, warmup: int, stream) -> float:
     """Mean ms per launch of `launch` over `steps` back-to-back launches on
     `stream`, timed with HIP events bracketed by device synchronisation.
+    Afterwards PER_LAUNCH more launches are timed one by one (an event pair
+    around each, on the same stream) and their median is left in
+    LAST_MEDIAN_MS.
     Before them: `warmup` untimed launches, then as many more as fill about
     SETTLE_MS (counted from the warm-up's own mean).  A heavy kernel started
     after a pause first runs at transient clocks on MI355X: the fp32 conv1d
@@ -98,7 +108,17 @@ def timed(launch, steps: int, warmup: int, stream) -> float:
         launch()
     end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    mean_ms = start.elapsed_time(end) / steps
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in range(PER_LAUNCH)]
+    for a, b in pairs:
+        a.record(stream)
+        launch()
+        b.record(stream)
+    torch.cuda.synchronize()
+    global LAST_MEDIAN_MS
+    LAST_MEDIAN_MS = statistics.median(a.elapsed_time(b) for a, b in pairs)
+    return mean_ms
 
 
 def time_gpu(T: str, forward: bool, steps: int, warmup: int, n: int = N_FFT,
@@ -123,7 +143,8 @@ def time_gpu(T: str, forward: bool, steps: int, warmup: int, n: int = N_FFT,
     del x, y
     return {
         "precision": T, "direction": "forward" if forward else "inverse", "n": n, "batch": batch,
-        "us_per_call": ms * 1e3, "us_per_transform": ms * 1e3 / batch,
+        "us_per_call": ms * 1e3, "median_us_per_call": LAST_MEDIAN_MS * 1e3,
+        "ns_per_transform": ms * 1e6 / batch,
         "gflops": flops / (ms * 1e-3) / 1e9,
         "gbps": nbytes / (ms * 1e-3) / 1e9,
         "pct_hbm_peak": 100.0 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
@@ -176,7 +197,8 @@ def time_conv(kind: str, T: str, steps: int, warmup: int) -> dict:
     del x, y, h
     return {"workload": (f"{kind} {batch} x {'2048' if kind == 'conv1d' else '64x64'} "
                          f"{T}2, fused FFT * H * IFFT"),
-            "precision": T, "us_per_call": ms * 1e3, "gflops": flops / (ms * 1e-3) / 1e9,
+            "precision": T, "us_per_call": ms * 1e3, "median_us_per_call": LAST_MEDIAN_MS * 1e3,
+            "gflops": flops / (ms * 1e-3) / 1e9,
             "gbps": nbytes / (ms * 1e-3) / 1e9,
             "pct_hbm_peak": 100.0 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
             "bytes_per_call": nbytes}
@@ -218,7 +240,8 @@ def time_conv_real(T: str, n: int, steps: int, warmup: int) -> dict:
     del x, y, h, spectrum
     return {"workload": (f"conv1d_real [{batch}][{channels}][{n}] {T}, 9-tap real filters, "
                          f"fused FFT * H * IFFT (two signals per complex transform)"),
-            "precision": T, "us_per_call": ms * 1e3, "gflops": flops / (ms * 1e-3) / 1e9,
+            "precision": T, "us_per_call": ms * 1e3, "median_us_per_call": LAST_MEDIAN_MS * 1e3,
+            "gflops": flops / (ms * 1e-3) / 1e9,
             "gbps": nbytes / (ms * 1e-3) / 1e9,
             "pct_hbm_peak": 100.0 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
             "bytes_per_call": nbytes}
@@ -254,7 +277,8 @@ def time_conv_valid(T: str, ntaps: int, steps: int, warmup: int) -> dict:
     del x, y, taps
     return {"workload": (f"conv1d_valid {length} x {ntaps} taps {T}2, 64-point windows "
                          f"({65 - ntaps} outputs each)"),
-            "precision": T, "us_per_call": ms * 1e3, "gflops": flops / (ms * 1e-3) / 1e9,
+            "precision": T, "us_per_call": ms * 1e3, "median_us_per_call": LAST_MEDIAN_MS * 1e3,
+            "gflops": flops / (ms * 1e-3) / 1e9,
             "gbps": nbytes / (ms * 1e-3) / 1e9,
             "pct_hbm_peak": 100.0 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
             "bytes_per_call": nbytes}
@@ -372,10 +396,99 @@ def cpu_baseline(target_s: float) -> dict:
     flops = 5.0 * n * math.log2(n) * sample
     del x
     return {"value": flops / dt / 1e9, "unit": "GFLOP/s", "cores": cores, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{sample} float forward transforms of N={n} (of the {BATCH}-signal "
                       f"workload), {reps} timed passes, {dt * 1e3:.1f} ms per pass, "
                       f"oracle fft_f32_fourstep on {cores} threads",
             "us_per_transform": dt * 1e6 / sample}
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or platform.machine()
+
+
+def sync_wrapper(T: str, calls: int = 25, warmup: int = 10) -> dict:
+    """The synchronous ThunderFFT_global wrapper as a caller sees it: host wall
+    time around each call (argument checks, the table lookup, the launch and
+    hipStreamSynchronize, plus the ctypes binding), median of `calls` calls
+    at N=1024, batch 65536."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    n, batch = N_FFT, BATCH
+    dt = torch.float32 if T == "float" else torch.float16
+    x = torch.empty(2 * n * batch, dtype=dt, device="cuda")
+    y = torch.empty_like(x)
+    stream = torch.cuda.current_stream()
+    thff.fill_uniform(T, x, n * batch, 0x7F4A7C15 + n, 0, stream)
+    thff.ThunderFFTInitialize(T, n)
+    for _ in range(warmup):
+        thff.ThunderFFT_global(T, n, True, x, y, batch, stream)
+    times = []
+    for _ in range(calls):
+        t0 = time.perf_counter()
+        thff.ThunderFFT_global(T, n, True, x, y, batch, stream)
+        times.append(time.perf_counter() - t0)
+    del x, y
+    return {"precision": T, "calls": calls, "median_us_per_call": statistics.median(times) * 1e6,
+            "min_us_per_call": min(times) * 1e6,
+            "note": "host wall clock around the synchronous wrapper, through ctypes"}
+
+
+def host_fp64_check(subset: int = 256) -> dict:
+    """The host fp64 check, timed on its own: the GPU's float forward transform
+    of the bench input (N=1024, batch 65536) against the oracle's fp64 radix-2
+    FFT of the same seeded input over the full batch (one thread), and that
+    FFT against the fp64 direct DFT on a `subset`-signal subset."""
+    import numpy as np
+    import torch
+
+    import oracle
+    import thunderfft_amd as thff
+
+    n, batch = N_FFT, BATCH
+    x_d = torch.empty(2 * n * batch, dtype=torch.float32, device="cuda")
+    y_d = torch.empty_like(x_d)
+    stream = torch.cuda.current_stream()
+    thff.fill_uniform("float", x_d, n * batch, 0x7F4A7C15 + n, 0, stream)
+    thff.ThunderFFTInitialize("float", n)
+    thff.ThunderFFT_global("float", n, True, x_d, y_d, batch, stream)
+    got = y_d.cpu().numpy().view(np.complex64).reshape(batch, n)
+    del x_d, y_d
+    x = oracle.uniform(n, batch)  # the generator the device fill uses
+    t0 = time.perf_counter()
+    ref = oracle.fft(x, True)
+    t_fft = time.perf_counter() - t0
+    rows = np.unique(np.linspace(0, batch - 1, subset).astype(np.int64))
+    t0 = time.perf_counter()
+    direct = oracle.dft(x[rows], True)
+    t_dft = time.perf_counter() - t0
+    fft_vs_dft = float(np.linalg.norm(ref[rows] - direct) / np.linalg.norm(direct))
+    err2 = ref2 = 0.0
+    for lo in range(0, batch, 4096):
+        r = ref[lo:lo + 4096]
+        err2 += float(np.sum(np.abs(got[lo:lo + 4096].astype(np.complex128) - r) ** 2))
+        ref2 += float(np.sum(np.abs(r) ** 2))
+    del ref, direct, got, x
+    return {"fp64_fft_s": t_fft, "fp64_fft_signals": batch, "direct_dft_s": t_dft,
+            "direct_dft_signals": int(len(rows)), "threads": 1,
+            "fp64_fft_vs_direct_dft_rel_l2": fft_vs_dft,
+            "gpu_float_fwd_vs_fp64_rel_l2": math.sqrt(err2 / ref2), "gate": 5e-3}
+
+
+def sig(v: float, digits: int = 6) -> float:
+    """v to `digits` significant figures (no loss for small values)."""
+    return float(f"{v:.{digits}g}")
 
 
 def _profile_value(path: str, field: str, key: str):
@@ -440,7 +553,7 @@ def sweep(a) -> None:
         for n in (64, 128, 256, 512, 1024, 2048, 4096):
             for fwd in (True, False):
                 r = time_gpu(T, fwd, a.steps, a.warmup, n, (1 << 26) // n)
-                out.append({k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()})
+                out.append({k: (sig(v) if isinstance(v, float) else v) for k, v in r.items()})
                 print(f"[sweep] {T} N={n} batch={(1 << 26) // n} {'forward' if fwd else 'inverse'}: "
                       f"{r['us_per_call']:.1f} us, {r['gbps']:.0f} GB/s "
                       f"({r['pct_hbm_peak']:.1f}% of HBM peak), {r['gflops']:.0f} GFLOP/s",
@@ -505,11 +618,26 @@ def main():
         runs[f"compute_{T}"] = r
         print(f"[bench] {T} N=1024 x 65536 differential compute (R={r['repeats']}): "
               f"{r['compute_us_per_pass']:.1f} us per pass", file=sys.stderr, flush=True)
+    for T in ("float", "half"):
+        r = sync_wrapper(T)
+        runs[f"sync_wrapper_{T}_fwd"] = r
+        print(f"[bench] {T} N=1024 x 65536 synchronous ThunderFFT_global: "
+              f"{r['median_us_per_call']:.1f} us per call (median of {r['calls']})",
+              file=sys.stderr, flush=True)
+    thff.ThunderFFTFinalize("float")
+    thff.ThunderFFTFinalize("half")
     copy_gbps, torch_copy_gbps = copy_bandwidth(a.steps, a.warmup)
     print(f"[bench] 512 MiB non-temporal copy: {copy_gbps:.0f} GB/s "
           f"({100.0 * copy_gbps / HBM_PEAK_GBPS:.1f}% of HBM peak); torch copy_ {torch_copy_gbps:.0f} GB/s",
           file=sys.stderr, flush=True)
     main_run = runs["float_fwd"]
+    fp64 = None
+    if not a.no_fp64_check:
+        fp64 = host_fp64_check()
+        print(f"[bench] host fp64 check: fp64 FFT of {fp64['fp64_fft_signals']} signals "
+              f"{fp64['fp64_fft_s']:.1f} s, direct DFT of {fp64['direct_dft_signals']} "
+              f"{fp64['direct_dft_s']:.2f} s; GPU float forward vs fp64 rel L2 "
+              f"{fp64['gpu_float_fwd_vs_fp64_rel_l2']:.3e}", file=sys.stderr, flush=True)
     cpu = None if a.no_cpu else cpu_baseline(a.cpu_seconds)
     achieved = main_run["gbps"]
     out = {
@@ -544,7 +672,10 @@ def main():
                      "kernel": "thff::c2c_kernel<float2, 1024, true, false, false>",
                      "algorithmic_bytes": main_run["bytes_per_call"]},
         "cpu_baseline": cpu,
-        "also": {k: {kk: (round(vv, 3) if isinstance(vv, float) else vv)
+        "host_fp64_check": ({k: (sig(v) if isinstance(v, float) else v) for k, v in fp64.items()}
+                            if fp64 else None),
+        "median_us_per_call": sig(main_run["median_us_per_call"]),
+        "also": {k: {kk: (sig(vv) if isinstance(vv, float) else vv)
                      for kk, vv in v.items()} for k, v in runs.items()},
     }
     for k in out["also"]:

@@ -111,6 +111,70 @@ def test_uninitialized_length_raises():
         thff.ThunderFFT_global("float", 128, True, x, y, 1)
 
 
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("n", SIZES)
+def test_element_aligned_buffers(T, n):
+    """Buffers that start on an odd element, not on a 16-byte boundary: the
+    reference takes any vec2_t<T> buffer (thunderfft_impl_kernel.cuh:18-21),
+    so these run the direct-movement kernel.  Input and/or output offset by 1
+    or 3 elements, a partial last tile; the elements around the output must
+    stay untouched."""
+    import thunderfft_amd as thff
+
+    esize = 8 if T == "float" else 4
+    batch = 2 * thff.transforms_per_block(n) + 3
+    count = batch * n
+    xr = oracle.represent(oracle.make_input(n, batch, 0), T)
+    thff.ThunderFFTInitialize(T, n)
+    for in_off, out_off in ((1, 3), (0, 1), (3, 0)):
+        host_in = np.zeros(count + in_off, np.complex64)
+        host_in[in_off:] = xr.reshape(-1)
+        d_in = to_device(host_in, T)
+        guard = np.complex64(-271.0 + 137.0j)
+        host_out = np.full(count + out_off + 16, guard, np.complex64)
+        host_out[out_off:out_off + count] = np.nan
+        d_out = to_device(host_out, T)
+        for forward in (True, False):
+            thff.ThunderFFT_global(T, n, forward, d_in.data_ptr() + in_off * esize,
+                                   d_out.data_ptr() + out_off * esize, batch)
+            out = from_device(d_out, T)
+            m = oracle.metrics(out[out_off:out_off + count], oracle.fft(xr, forward).reshape(-1))
+            label = f"{T} N={n} offsets in={in_off} out={out_off} {'fwd' if forward else 'inv'}"
+            print(f"{label}: rel_l2={m['rel_l2']:.3e}", flush=True)
+            assert m["nonfinite"] == 0 and m["rel_l2"] <= GATE and m["rel_l2"] <= TIGHT[T], label
+            around = np.concatenate([out[:out_off], out[out_off + count:]])
+            assert np.all(around == guard), label
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+def test_fft_convenience(T):
+    """thunderfft_amd.fft: complex64 / float16[..., N, 2] tensors, with and
+    without a caller's out, against the oracle; the length that was current
+    for T before the call is current again afterwards."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    thff.ThunderFFTInitialize(T, 256)
+    for n in (64, 1024):
+        xr = oracle.represent(oracle.make_input(n, 5, 2), T)
+        if T == "float":
+            x = torch.from_numpy(xr).cuda()
+        else:
+            x = to_device(xr, T).view(5, n, 2)
+        for forward in (True, False):
+            y = thff.fft(x, forward=forward)
+            out = torch.empty_like(x)
+            y2 = thff.fft(x, forward=forward, out=out)
+            assert y2 is out
+            torch.cuda.synchronize()
+            for got in (y, y2):
+                host = got.cpu().numpy() if T == "float" else from_device(got.reshape(-1), T)
+                m = oracle.metrics(host.reshape(-1), oracle.fft(xr, forward).reshape(-1))
+                assert m["nonfinite"] == 0 and m["rel_l2"] <= TIGHT[T], (n, forward)
+        assert thff.twiddle_info(T)[1] == 256
+
+
 def test_twiddle_cache_lifecycle():
     """sample/validation/cache_validation.cu:65-121 on the current device."""
     import torch

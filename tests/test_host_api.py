@@ -158,20 +158,55 @@ def test_conv1d_valid_argument_checks():
 
 
 def test_misaligned_buffers_rejected():
-    """The kernels move 16-byte vectors, so every entry point rejects buffers
-    that do not start on a 16-byte boundary (THFF_EINVAL, before any HIP
-    call).  The reference takes any pointer; hipMalloc'd buffers and offsets
-    of whole transforms are always aligned."""
-    for T in ("float", "half"):
-        for x, y in ((24, 48), (16, 40), (20, 48)):
-            with pytest.raises(ValueError, match="16-byte aligned"):
+    """The convolutions move 16-byte vectors, so they reject buffers that do
+    not start on a 16-byte boundary (THFF_EINVAL, before any HIP call).
+    ThunderFFT_global takes any vec2_t<T> buffer, as the reference does: it
+    rejects only buffers below the element's alignment (8 bytes for float2, 4
+    for half2); element-aligned ones pass the argument checks."""
+    for T, bad, elem_aligned in (("float", 20, 24), ("half", 18, 20)):
+        for x, y in ((bad, 48), (16, bad + 32)):
+            with pytest.raises(ValueError, match="aligned"):
                 thff.ThunderFFT_global(T, 64, True, x, y, 1)
+        # Past the argument checks: no table is live (none can be without a GPU),
+        # so the call fails with the runtime error, not ValueError.
+        try:
+            thff.ThunderFFTFinalize(T)
+        except RuntimeError:
+            pass
+        with pytest.raises(RuntimeError):
+            thff.ThunderFFT_global(T, 64, True, elem_aligned, 48, 1)
         with pytest.raises(ValueError, match="16-byte aligned"):
             thff.ThunderFFT_conv1d(T, 64, 16, 24, 48, 1)
         with pytest.raises(ValueError, match="16-byte aligned"):
             thff.ThunderFFT_conv1d(T, 64, 16, 32, 56, 1, False)
         with pytest.raises(ValueError, match="16-byte aligned"):
             thff.ThunderFFT_conv2d(T, 64, 64, 24, 32, 48, 1)
+
+
+def test_fft_convenience_argument_checks():
+    """fft() checks its arguments before any HIP call: dtype and shape, the
+    length, and a caller's `out` (dtype, shape, device, contiguity, overlap);
+    host tensors are refused last (there is no CPU path)."""
+    torch = pytest.importorskip("torch")
+    x = torch.zeros(4, 64, dtype=torch.complex64)
+    with pytest.raises(ValueError, match="complex64 or float16"):
+        thff.fft(torch.zeros(4, 64, dtype=torch.float32))
+    with pytest.raises(ValueError, match="unsupported FFT size"):
+        thff.fft(torch.zeros(4, 100, dtype=torch.complex64))
+    with pytest.raises(ValueError, match="unsupported FFT size"):
+        thff.fft(torch.zeros(4, 96, 2, dtype=torch.float16))
+    bad_outs = [torch.zeros(4, 64, dtype=torch.complex128), torch.zeros(2, 64, dtype=torch.complex64),
+                torch.zeros(64, 4, dtype=torch.complex64).t()]
+    for out in bad_outs:
+        with pytest.raises(ValueError, match="out must"):
+            thff.fft(x, out=out)
+    with pytest.raises(ValueError, match="overlap"):
+        thff.fft(x, out=x)
+    big = torch.zeros(8, 64, dtype=torch.complex64)
+    with pytest.raises(ValueError, match="overlap"):
+        thff.fft(big[:4], out=big[2:6])
+    with pytest.raises(ValueError, match="device tensor"):
+        thff.fft(x, out=torch.zeros_like(x))
 
 
 def test_copy_nt_argument_checks():

@@ -248,8 +248,12 @@ def transforms_per_block(N: int) -> int:
 def fft(x, forward: bool = True, out=None):
     """Transform the last axis of a CUDA tensor (complex64 or float16[..., N, 2]).
 
-    A convenience over ThunderFFT_global: initialises the twiddle table for
-    (T, N) on the tensor's device if needed and returns a new tensor.
+    A convenience over ThunderFFT_global.  ``out``, when given, must match
+    ``x`` in dtype, shape and device, be contiguous and not overlap ``x``;
+    every argument is checked (ValueError) before any HIP call.  The table for
+    (T, N) is initialised on the tensor's device if needed, and the length
+    that was current for T before the call is made current again afterwards
+    (its table is kept, so that costs no allocation).
     """
     import torch
 
@@ -259,14 +263,32 @@ def fft(x, forward: bool = True, out=None):
         T, n = "half", x.shape[-2]
     else:
         raise ValueError("fft expects complex64 or float16[..., N, 2] tensors")
+    if n not in SUPPORTED_N:
+        raise ValueError(f"fft: unsupported FFT size {n} (supported: {SUPPORTED_N})")
+    if out is not None:
+        if out.dtype != x.dtype or tuple(out.shape) != tuple(x.shape) or out.device != x.device:
+            raise ValueError("fft: out must match x in dtype, shape and device")
+        if not out.is_contiguous():
+            raise ValueError("fft: out must be contiguous")
+        nbytes = x.numel() * x.element_size()
+        if nbytes and (x.data_ptr() < out.data_ptr() + nbytes and
+                       out.data_ptr() < x.data_ptr() + nbytes):
+            raise ValueError("fft: out must not overlap x")
     if not x.is_cuda:
         raise ValueError("fft expects a device tensor (there is no CPU path)")
     x = x.contiguous()
     if out is None:
         out = torch.empty_like(x)
     batch = x.numel() // (n * (2 if T == "half" else 1))
+    if batch == 0:
+        return out
     with torch.cuda.device(x.device):
-        if twiddle_info(T)[1] != n:
+        previous = twiddle_info(T)[1]
+        if previous != n:
             ThunderFFTInitialize(T, n)
-        ThunderFFT_global(T, n, forward, x, out, batch, torch.cuda.current_stream(x.device))
+        try:
+            ThunderFFT_global(T, n, forward, x, out, batch, torch.cuda.current_stream(x.device))
+        finally:
+            if previous not in (0, n):
+                ThunderFFTInitialize(T, previous)
     return out

@@ -1,155 +1,146 @@
-// thff_fft -- the quick-start check of the reference's sample/fft1d/main.cu
-// (`thff_fft`) on MI355X:
+// thff_fft -- quick-start check of the public API on MI355X:
 //
 //   thff_fft [batch] [device]
 //
-// One unscaled, out-of-place, complex float forward transform of N=64 over
-// `batch` signals (a positive multiple of 16, default 16) on HIP device
-// `device` (default 0), through ThunderFFTInitialize<float>(64) and
-// ThunderFFT_global<float, 64, true>, compared with hipFFT's single-precision
-// C2C transform of the same input (the reference compares with cuFFT C2C).
+// Transforms `batch` example signals of N = 64 (batch a positive multiple of
+// 16, default 16) forward, unscaled and out of place with
+// ThunderFFT_global<float, 64, true> on HIP device `device` (default 0), and
+// compares the result with hipFFT's single-precision C2C transform of the
+// same input.
 //
-// The input is the reference's deterministic one (main.cu:63-77): signal b
-// holds a bin-aligned tone of frequency 1 + b % 13 and amplitude
-// 0.5 + 0.1 * (b % 8), plus a tone of amplitude 0.1 at bin 7.
-//
-// Output and exit status follow main.cu:153-193: the configuration line,
-// "Relative L2", "Relative Linf" and "Tolerance" in scientific notation,
-// then PASS or FAIL.  PASS needs finite outputs and both relative errors
-// <= 5e-3.  Invalid arguments, HIP/hipFFT errors, nonfinite values and a
-// failed comparison all exit 1 ("FAIL: <reason>" on stderr for the first
-// three); --help / -h prints the usage and exits 0.  Arguments are checked
-// before any HIP call.
-#include <hipfft/hipfft.h>
+// Command-line contract of the reference's quick start (sample/fft1d/main.cu:
+// arguments :170-193, example input :63-77, report :153-160): the same
+// arguments, report lines and exit codes.  PASS needs finite values and both
+// relative L2 and relative Linf <= 5e-3; a failed comparison, invalid
+// arguments (checked before any HIP call), HIP/hipFFT errors and nonfinite
+// values exit 1, the last three with "FAIL: <reason>" on stderr; --help or
+// -h prints the usage and exits 0.
 #include <thunderfft/thunderfft.cuh>
 
-#include <algorithm>
-#include <charconv>
-#include <cmath>
-#include <cstdlib>
+#include "cli_common.hpp"
+
+#include <climits>
+#include <complex>
 #include <cstring>
 #include <iomanip>
 #include <iostream>
-#include <limits>
 #include <stdexcept>
 #include <string>
 #include <vector>
 
 namespace {
 
-constexpr int kN = 64;                // main.cu:21
-constexpr int kSignalsPerTile = 16;   // main.cu:22: the batch granularity the sample accepts
-constexpr double kGate = 5e-3;        // main.cu:24
+using thff_cli::DeviceArray;
+using thff_cli::ErrorStats;
 
-void hip_ok(hipError_t e, const char* what) {
-    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+constexpr int kLength = 64;
+constexpr int kBatchGranule = 16;  // the example accepts whole 16-signal groups
+constexpr double kGate = 5e-3;
+
+struct Request {
+    int batch = kBatchGranule;
+    int device = 0;
+};
+
+const char* const kUsage =
+    " [batch] [device]\n"
+    "  batch   Positive multiple of 16 (default: 16).\n"
+    "  device  Nonnegative HIP device ordinal (default: 0).\n"
+    "Checks an unscaled, out-of-place, complex float forward FFT (N=64) against hipFFT.\n"
+    "PASS requires finite outputs and relative L2/Linf <= 5e-3 for this example input.\n";
+
+int nonnegative(const char* text, const char* what) {
+    int value = 0;
+    if (!thff_cli::parse_decimal(text, 0, INT_MAX, value) || text[0] == '+')
+        throw std::invalid_argument(std::string(what) +
+                                    " must be a nonnegative integer in int range");
+    return value;
 }
 
-void fft_ok(hipfftResult e, const char* what) {
-    if (e != HIPFFT_SUCCESS)
-        throw std::runtime_error(std::string(what) + ": hipFFT status " +
-                                 std::to_string(static_cast<int>(e)));
+// Positional arguments -> request; every rule is checked before any HIP call.
+Request read_request(int argc, char** argv) {
+    if (argc > 3) throw std::invalid_argument("too many arguments");
+    Request r;
+    if (argc >= 2) r.batch = nonnegative(argv[1], "batch");
+    if (argc >= 3) r.device = nonnegative(argv[2], "device");
+    if (r.batch == 0 || r.batch % kBatchGranule != 0)
+        throw std::invalid_argument("batch must be a positive multiple of 16");
+    return r;
 }
 
-void usage(std::ostream& os, const char* prog) {
-    os << "Usage: " << prog << " [batch] [device]\n"
-       << "  batch   Positive multiple of 16 (default: 16).\n"
-       << "  device  Nonnegative HIP device ordinal (default: 0).\n"
-       << "Checks an unscaled, out-of-place, complex float forward FFT (N=64) against hipFFT.\n"
-       << "PASS requires finite outputs and relative L2/Linf <= 5e-3 for this example input.\n";
-}
-
-int parse_count(const char* text, const char* name) {
-    int v = 0;
-    const char* end = text + std::strlen(text);
-    const auto r = std::from_chars(text, end, v);
-    if (r.ec != std::errc{} || r.ptr != end || v < 0)
-        throw std::invalid_argument(std::string(name) + " must be a nonnegative integer in int range");
-    return v;
-}
-
-// Signal b: a * e^{i f theta} + 0.1 * e^{i 7 theta}, theta = 2 pi n / N,
-// f = 1 + b % 13, a = 0.5 + 0.1 * (b % 8); evaluated in double, stored as float.
-std::vector<float2> tones(int batch) {
-    std::vector<float2> x(static_cast<size_t>(batch) * kN);
+// Signal b: a tone of amplitude 0.5 + 0.1 (b mod 8) on bin 1 + (b mod 13)
+// plus a tone of amplitude 0.1 on bin 7, evaluated in double and stored as
+// float (the reference's example input).
+std::vector<float2> example_signals(int batch) {
+    std::vector<float2> signals;
+    signals.reserve(static_cast<size_t>(batch) * kLength);
     for (int b = 0; b < batch; ++b) {
-        const double f = 1 + b % 13, a = 0.5 + 0.1 * (b % 8);
-        for (int n = 0; n < kN; ++n) {
-            const double theta = 2.0 * M_PI * n / kN;
-            x[static_cast<size_t>(b) * kN + n] =
-                make_float2(static_cast<float>(a * std::cos(f * theta) + 0.1 * std::cos(7.0 * theta)),
-                            static_cast<float>(a * std::sin(f * theta) + 0.1 * std::sin(7.0 * theta)));
+        const double amplitude = 0.5 + 0.1 * (b % 8);
+        const int bin = 1 + b % 13;
+        for (int n = 0; n < kLength; ++n) {
+            const double theta = 2.0 * M_PI * n / kLength;
+            const std::complex<double> v =
+                std::polar(amplitude, bin * theta) + std::polar(0.1, 7.0 * theta);
+            signals.push_back(make_float2(static_cast<float>(v.real()),
+                                          static_cast<float>(v.imag())));
         }
     }
-    return x;
+    return signals;
 }
 
-// Owns every device resource so that an exception on any step releases them.
-struct Session {
-    float2* in = nullptr;
-    float2* out = nullptr;
-    float2* ref = nullptr;
-    hipfftHandle plan = 0;
-    bool plan_made = false;
-    bool initialized = false;
-    ~Session() {
-        if (plan_made) (void)hipfftDestroy(plan);
-        if (initialized) thunderfft::ThunderFFTFinalize<float>();
-        if (ref) (void)hipFree(ref);
-        if (out) (void)hipFree(out);
-        if (in) (void)hipFree(in);
+// Makes the twiddle table live for the scope and releases it on every exit.
+struct LiveTable {
+    LiveTable() { thunderfft::ThunderFFTInitialize<float>(kLength); }
+    ~LiveTable() {
+        try {
+            thunderfft::ThunderFFTFinalize<float>();
+        } catch (...) {
+        }
     }
 };
 
-bool run(int batch, int device) {
-    hip_ok(hipSetDevice(device), "hipSetDevice");
-    const size_t count = static_cast<size_t>(kN) * batch, bytes = count * sizeof(float2);
-    const std::vector<float2> x = tones(batch);
-    std::vector<float2> y(count), r(count);
-
-    Session s;
-    hip_ok(hipMalloc(&s.in, bytes), "hipMalloc(input)");
-    hip_ok(hipMalloc(&s.out, bytes), "hipMalloc(output)");
-    hip_ok(hipMalloc(&s.ref, bytes), "hipMalloc(reference)");
-    hip_ok(hipMemcpy(s.in, x.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy(input)");
-
-    s.initialized = true;
-    thunderfft::ThunderFFTInitialize<float>(kN);
-    hip_ok(hipGetLastError(), "ThunderFFTInitialize");
-    hip_ok(hipDeviceSynchronize(), "ThunderFFTInitialize synchronization");
-
-    thunderfft::ThunderFFT_global<float, kN, true>(s.in, s.out, batch, /*stream=*/0);
-    hip_ok(hipGetLastError(), "ThunderFFT launch");
-    hip_ok(hipDeviceSynchronize(), "ThunderFFT synchronization");
-
-    fft_ok(hipfftPlan1d(&s.plan, kN, HIPFFT_C2C, batch), "hipfftPlan1d");
-    s.plan_made = true;
-    fft_ok(hipfftExecC2C(s.plan, reinterpret_cast<hipfftComplex*>(s.in),
-                         reinterpret_cast<hipfftComplex*>(s.ref), HIPFFT_FORWARD),
-           "hipfftExecC2C");
-    hip_ok(hipGetLastError(), "hipFFT launch");
-    hip_ok(hipDeviceSynchronize(), "hipFFT synchronization");
-    hip_ok(hipMemcpy(y.data(), s.out, bytes, hipMemcpyDeviceToHost), "hipMemcpy(output)");
-    hip_ok(hipMemcpy(r.data(), s.ref, bytes, hipMemcpyDeviceToHost), "hipMemcpy(reference)");
-
-    double err2 = 0.0, ref2 = 0.0, err_max = 0.0, ref_max = 0.0;
-    for (size_t i = 0; i < count; ++i) {
-        if (!std::isfinite(y[i].x) || !std::isfinite(y[i].y) || !std::isfinite(r[i].x) ||
-            !std::isfinite(r[i].y))
-            throw std::runtime_error("nonfinite output at complex element " + std::to_string(i));
-        const double e = std::hypot(double(y[i].x) - r[i].x, double(y[i].y) - r[i].y);
-        const double m = std::hypot(double(r[i].x), double(r[i].y));
-        err2 += e * e;
-        ref2 += m * m;
-        err_max = std::max(err_max, e);
-        ref_max = std::max(ref_max, m);
+// Both transforms of the example input; returns {ours, hipFFT's}.
+std::pair<std::vector<float2>, std::vector<float2>> transform_both(const Request& r) {
+    thff_cli::hip_check(hipSetDevice(r.device), "hipSetDevice");
+    const std::vector<float2> input = example_signals(r.batch);
+    DeviceArray<float2> in(input.size(), "hipMalloc(input)");
+    DeviceArray<float2> ours(input.size(), "hipMalloc(output)");
+    DeviceArray<float2> theirs(input.size(), "hipMalloc(reference)");
+    in.upload(input, "hipMemcpy(input)");
+    {
+        const LiveTable table;
+        // synchronous: returns once the transform has finished, throws on failure
+        thunderfft::ThunderFFT_global<float, kLength, true>(in.get(), ours.get(), r.batch);
     }
-    const double l2 = ref2 > 0.0 ? std::sqrt(err2 / ref2) : std::sqrt(err2);
-    const double linf = ref_max > 0.0 ? err_max / ref_max : err_max;
+    const thff_cli::FftPlan plan(kLength, HIPFFT_C2C, r.batch);
+    thff_cli::fft_check(hipfftExecC2C(plan.get(), reinterpret_cast<hipfftComplex*>(in.get()),
+                                      reinterpret_cast<hipfftComplex*>(theirs.get()),
+                                      HIPFFT_FORWARD),
+                        "hipfftExecC2C");
+    thff_cli::hip_check(hipDeviceSynchronize(), "hipFFT synchronization");
+    return {ours.download("hipMemcpy(output)"), theirs.download("hipMemcpy(reference)")};
+}
+
+ErrorStats compare(const std::vector<float2>& ours, const std::vector<float2>& theirs) {
+    ErrorStats stats, reference_finite;
+    for (size_t i = 0; i < ours.size(); ++i) {
+        stats.add(ours[i].x, ours[i].y, theirs[i].x, theirs[i].y);
+        reference_finite.add(theirs[i].x, theirs[i].y, 0, 0);
+    }
+    if (stats.nonfinite || reference_finite.nonfinite)
+        throw std::runtime_error("nonfinite output (" + std::to_string(stats.nonfinite) +
+                                 " ThunderFFT, " + std::to_string(reference_finite.nonfinite) +
+                                 " hipFFT values)");
+    return stats;
+}
+
+bool report(const Request& r, const ErrorStats& stats) {
+    const double l2 = stats.rel_l2(), linf = stats.rel_linf();
     const bool pass = std::isfinite(l2) && std::isfinite(linf) && l2 <= kGate && linf <= kGate;
-    std::cout << "ThunderFFT vs hipFFT: float2, N=" << kN << ", forward (unscaled), batch=" << batch
-              << ", device=" << device << '\n'
-              << std::scientific << std::setprecision(6) << "Relative L2:   " << l2 << '\n'
+    std::cout << "ThunderFFT vs hipFFT: float2, N=" << kLength << ", forward (unscaled), batch="
+              << r.batch << ", device=" << r.device << '\n'
+              << std::scientific << std::setprecision(6)
+              << "Relative L2:   " << l2 << '\n'
               << "Relative Linf: " << linf << '\n'
               << "Tolerance:     " << kGate << " (this example input)\n"
               << (pass ? "PASS" : "FAIL") << '\n';
@@ -159,21 +150,16 @@ bool run(int batch, int device) {
 }  // namespace
 
 int main(int argc, char** argv) {
-    if (argc == 2 && (std::strcmp(argv[1], "--help") == 0 || std::strcmp(argv[1], "-h") == 0)) {
-        usage(std::cout, argv[0]);
-        return EXIT_SUCCESS;
+    if (argc == 2 && (!std::strcmp(argv[1], "--help") || !std::strcmp(argv[1], "-h"))) {
+        std::cout << "Usage: " << argv[0] << kUsage;
+        return 0;
     }
     try {
-        if (argc > 3) throw std::invalid_argument("too many arguments");
-        const int batch = argc > 1 ? parse_count(argv[1], "batch") : kSignalsPerTile;
-        const int device = argc > 2 ? parse_count(argv[2], "device") : 0;
-        if (batch <= 0 || batch % kSignalsPerTile != 0)
-            throw std::invalid_argument("batch must be a positive multiple of 16");
-        if (static_cast<size_t>(batch) > std::numeric_limits<size_t>::max() / (kN * sizeof(float2)))
-            throw std::invalid_argument("batch allocation size overflows size_t");
-        return run(batch, device) ? EXIT_SUCCESS : EXIT_FAILURE;
+        const Request request = read_request(argc, argv);
+        const auto [ours, theirs] = transform_both(request);
+        return report(request, compare(ours, theirs)) ? 0 : 1;
     } catch (const std::exception& e) {
         std::cerr << "FAIL: " << e.what() << '\n';
-        return EXIT_FAILURE;
+        return 1;
     }
 }

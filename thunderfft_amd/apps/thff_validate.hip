@@ -18,13 +18,15 @@
 // * One CSV line per case on stdout (and --csv PATH), with the reference's
 //   columns.  Exit codes: 0 pass, 1 numerical/guard failure, 2 usage or
 //   HIP/hipFFT error.
-#include <hipfft/hipfft.h>
 #include <thunderfft/thunderfft.cuh>
+
+#include "cli_common.hpp"
 
 #include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <fstream>
+#include <functional>
 #include <iostream>
 #include <random>
 #include <sstream>
@@ -42,22 +44,8 @@ constexpr float kLdsGuardRe = 299.f, kLdsGuardIm = -299.f;
 constexpr const char* kKindNames[4] = {"gaussian_rms1", "offset_impulse", "complex_tone",
                                        "constant"};
 
-void hip_ok(hipError_t e, const char* what) {
-    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
-}
-void fft_ok(hipfftResult e, const char* what) {
-    if (e != HIPFFT_SUCCESS) throw std::runtime_error(std::string(what) + ": hipFFT error " +
-                                                      std::to_string(static_cast<int>(e)));
-}
-
-template <class V>
-struct Device {
-    V* p = nullptr;
-    explicit Device(size_t count) { hip_ok(hipMalloc(&p, count * sizeof(V)), "hipMalloc"); }
-    ~Device() { (void)hipFree(p); }
-    Device(const Device&) = delete;
-    Device& operator=(const Device&) = delete;
-};
+using thff_cli::DeviceArray;
+using thff_cli::hip_check;
 
 template <class T>
 __host__ __device__ vec2_t<T> store_as(float re, float im) {
@@ -178,59 +166,51 @@ void run_case(Report& rep, bool direct, int batch, int kind) {
         const float2 r = load_as<T>(x[i]);
         ref[i] = make_double2(r.x, r.y);
     }
-    Device<vec2_t<T>> d_in(count), d_out(count + kOutGuard);
-    Device<double2> d_ref(count);
-    Device<int> d_guard(1);
-    hip_ok(hipMemcpy(d_in.p, x.data(), count * sizeof(vec2_t<T>), hipMemcpyHostToDevice), "copy in");
+    // output: NaN-prefilled, then kOutGuard sentinels that must survive
     std::vector<vec2_t<T>> y(count + kOutGuard, store_as<T>(NAN, NAN));
     for (int g = 0; g < kOutGuard; ++g) y[count + g] = store_as<T>(kOutGuardRe, kOutGuardIm);
-    hip_ok(hipMemcpy(d_out.p, y.data(), y.size() * sizeof(vec2_t<T>), hipMemcpyHostToDevice), "prefill");
-    hip_ok(hipMemset(d_guard.p, 0, sizeof(int)), "guard reset");
+    DeviceArray<vec2_t<T>> d_in(count), d_out(y.size());
+    DeviceArray<double2> d_ref(count);
+    DeviceArray<int> d_guard(1);
+    d_in.upload(x, "copy in");
+    d_out.upload(y, "prefill");
+    d_ref.upload(ref, "copy ref");
+    d_guard.upload(std::vector<int>{0}, "guard reset");
 
-    // reference: fp64 Z2Z, unnormalized both ways
-    hip_ok(hipMemcpy(d_ref.p, ref.data(), count * sizeof(double2), hipMemcpyHostToDevice), "copy ref");
-    hipfftHandle plan;
-    fft_ok(hipfftPlan1d(&plan, N, HIPFFT_Z2Z, batch), "hipfftPlan1d");
-    const hipfftResult fr = hipfftExecZ2Z(plan, reinterpret_cast<hipfftDoubleComplex*>(d_ref.p),
-                                          reinterpret_cast<hipfftDoubleComplex*>(d_ref.p),
-                                          FWD ? HIPFFT_FORWARD : HIPFFT_BACKWARD);
-    (void)hipfftDestroy(plan);
-    fft_ok(fr, "hipfftExecZ2Z");
-
+    // reference: fp64 Z2Z in place, unnormalized both ways
+    {
+        const thff_cli::FftPlan plan(N, HIPFFT_Z2Z, batch);
+        auto* z = reinterpret_cast<hipfftDoubleComplex*>(d_ref.get());
+        thff_cli::fft_check(hipfftExecZ2Z(plan.get(), z, z, FWD ? HIPFFT_FORWARD : HIPFFT_BACKWARD),
+                            "hipfftExecZ2Z");
+    }
     if (direct) {
         constexpr int BPB = thunderfft::batch_per_block<N>;
         direct_core<T, N, FWD><<<(batch + BPB - 1) / BPB, 256>>>(
-            d_in.p, d_out.p, batch, thunderfft::ThunderFFT_twiddle_table<T>(), d_guard.p);
-        hip_ok(hipGetLastError(), "direct_core launch");
-        hip_ok(hipDeviceSynchronize(), "direct_core");
+            d_in.get(), d_out.get(), batch, thunderfft::ThunderFFT_twiddle_table<T>(),
+            d_guard.get());
+        hip_check(hipGetLastError(), "direct_core launch");
+        hip_check(hipDeviceSynchronize(), "direct_core");
     } else {
-        thunderfft::ThunderFFT_global<T, N, FWD>(d_in.p, d_out.p, batch);
+        thunderfft::ThunderFFT_global<T, N, FWD>(d_in.get(), d_out.get(), batch);
     }
-    hip_ok(hipMemcpy(y.data(), d_out.p, y.size() * sizeof(vec2_t<T>), hipMemcpyDeviceToHost), "copy out");
-    hip_ok(hipMemcpy(ref.data(), d_ref.p, count * sizeof(double2), hipMemcpyDeviceToHost), "copy ref out");
-    int lds_guard = 0;
-    hip_ok(hipMemcpy(&lds_guard, d_guard.p, sizeof(int), hipMemcpyDeviceToHost), "copy guard");
+    y = d_out.download("copy out");
+    ref = d_ref.download("copy ref out");
+    const int lds_guard = d_guard.download("copy guard")[0];
 
-    double err2 = 0, ref2 = 0, max_abs = 0, ref_max = 0;
-    long nonfinite = 0;
+    thff_cli::ErrorStats stats;
     for (size_t i = 0; i < count; ++i) {
         const float2 v = load_as<T>(y[i]);
-        if (!std::isfinite(v.x) || !std::isfinite(v.y)) ++nonfinite;
-        const double dx = v.x - ref[i].x, dy = v.y - ref[i].y;
-        err2 += dx * dx + dy * dy;
-        ref2 += ref[i].x * ref[i].x + ref[i].y * ref[i].y;
-        max_abs = std::fmax(max_abs, std::hypot(dx, dy));
-        ref_max = std::fmax(ref_max, std::hypot(ref[i].x, ref[i].y));
+        stats.add(v.x, v.y, ref[i].x, ref[i].y);
     }
     int out_guard = 0;
     for (int g = 0; g < kOutGuard; ++g) {
         const float2 v = load_as<T>(y[count + g]);
         out_guard += v.x != kOutGuardRe || v.y != kOutGuardIm;
     }
-    const double rel_l2 = ref2 > 0 ? std::sqrt(err2 / ref2) : std::sqrt(err2);
-    const double rel_linf = ref_max > 0 ? max_abs / ref_max : max_abs;
-    const bool pass = nonfinite == 0 && std::isfinite(rel_l2) && rel_l2 <= kGate && lds_guard == 0 &&
-                      out_guard == 0;
+    const double rel_l2 = stats.rel_l2();
+    const bool pass = stats.nonfinite == 0 && std::isfinite(rel_l2) && rel_l2 <= kGate &&
+                      lds_guard == 0 && out_guard == 0;
     ++rep.cases;
     rep.failures += pass ? 0 : 1;
     std::ostringstream s;
@@ -238,14 +218,14 @@ void run_case(Report& rep, bool direct, int batch, int kind) {
     s << std::scientific << (direct ? "direct" : "public") << ','
       << (std::is_same_v<T, float> ? "fp32" : "fp16") << ',' << N << ','
       << (FWD ? "forward" : "inverse") << ',' << kKindNames[kind] << ',' << batch << ',' << rel_l2
-      << ',' << max_abs << ',' << rel_linf << ',' << nonfinite << ',' << lds_guard << ','
-      << out_guard << ',' << (pass ? 1 : 0);
+      << ',' << stats.max_err << ',' << stats.rel_linf() << ',' << stats.nonfinite << ','
+      << lds_guard << ',' << out_guard << ',' << (pass ? 1 : 0);
     rep.line(s.str());
 }
 
 struct Options {
     int device = 0, batch = 64;
-    bool quick = false, host_only = false, batch_set = false;
+    bool quick = false, host_only = false, batch_set = false, help = false;
     std::string csv;
 };
 
@@ -287,93 +267,111 @@ void run_type(Report& rep, const Options& o) {
 }
 
 // ---------------------------------------------------------------- host checks
-int g_checks = 0;
-
-template <class Operation>
-void expect_invalid_argument(Operation operation, const char* description) {
-    try {
-        operation();
-    } catch (const std::invalid_argument&) {
-        ++g_checks;
-        return;
-    }
-    throw std::runtime_error(std::string("Host API check did not reject ") + description);
-}
+// The public API's argument contract (fft_validation.cu:331-352): each entry
+// is a call and whether it must be rejected with std::invalid_argument (or
+// return normally).  Every one is decided before the library makes a HIP
+// call, so the list runs on a machine without a GPU; the host addresses used
+// appear only where they must be rejected.
+struct HostCheck {
+    std::string what;
+    bool rejected;
+    std::function<void()> call;
+};
 
 template <class T>
-void host_checks() {
-    // Host pointers appear only in calls that must reject them for nullness
-    // or aliasing; none of these calls may reach the device.
-    vec2_t<T> value{};
-    expect_invalid_argument([] { thunderfft::ThunderFFT_global<T, 64>(nullptr, nullptr, -1); },
-                            "negative batch");
-    expect_invalid_argument([&] { thunderfft::ThunderFFT_global<T, 64>(nullptr, &value, 1); },
-                            "null input");
-    expect_invalid_argument([&] { thunderfft::ThunderFFT_global<T, 64>(&value, nullptr, 1); },
-                            "null output");
-    expect_invalid_argument([&] { thunderfft::ThunderFFT_global<T, 64>(&value, &value, 1); },
-                            "aliased input/output");
-    thunderfft::ThunderFFT_global<T, 64>(nullptr, nullptr, 0);
-    ++g_checks;
+std::vector<HostCheck> host_checks() {
+    static vec2_t<T> host_value{};
+    vec2_t<T>* const p = &host_value;
+    const std::string t = std::is_same_v<T, float> ? "float: " : "half: ";
+    std::vector<HostCheck> list = {
+        {t + "negative batch", true,
+         [] { thunderfft::ThunderFFT_global<T, 64>(nullptr, nullptr, -1); }},
+        {t + "null input", true, [p] { thunderfft::ThunderFFT_global<T, 64>(nullptr, p, 1); }},
+        {t + "null output", true, [p] { thunderfft::ThunderFFT_global<T, 64>(p, nullptr, 1); }},
+        {t + "aliased input/output", true, [p] { thunderfft::ThunderFFT_global<T, 64>(p, p, 1); }},
+        {t + "zero batch returns before touching pointers", false,
+         [] { thunderfft::ThunderFFT_global<T, 64>(nullptr, nullptr, 0); }},
+    };
     for (int n : {-1, 0, 32, 8192})
-        expect_invalid_argument([n] { thunderfft::ThunderFFTInitialize<T>(n); },
-                                "unsupported initialization length");
+        list.push_back({t + "Initialize(" + std::to_string(n) + ")", true,
+                        [n] { thunderfft::ThunderFFTInitialize<T>(n); }});
+    return list;
 }
 
-int parse_int(const char* text, const char* what) {
-    char* end = nullptr;
-    const long v = std::strtol(text, &end, 10);
-    if (!*text || *end || v < -2147483647L || v > 2147483647L)
+int run_host_checks() {
+    std::vector<HostCheck> all = host_checks<float>();
+    for (HostCheck& c : host_checks<half>()) all.push_back(std::move(c));
+    int passed = 0;
+    for (const HostCheck& c : all) {
+        bool rejected = false;
+        try {
+            c.call();
+        } catch (const std::invalid_argument&) {
+            rejected = true;
+        }
+        if (rejected != c.rejected)
+            throw std::runtime_error(std::string("Host API check ") +
+                                     (c.rejected ? "did not reject " : "rejected ") + c.what);
+        ++passed;
+    }
+    return passed;
+}
+
+// ---------------------------------------------------------------- options
+int int_option(const std::string& text, const char* what) {
+    int v = 0;
+    if (!thff_cli::parse_decimal(text, INT32_MIN + 1LL, INT32_MAX, v))
         throw std::runtime_error(std::string("Invalid ") + what + ": " + text);
-    return static_cast<int>(v);
+    return v;
 }
 
-void usage(const char* exe) {
-    std::cout << "Usage: " << exe << " [--device N] [--batch N] [--csv PATH] [--quick] [--host-only]\n"
-              << "All seven lengths, fp32/fp16, forward/inverse, direct (device API) and public\n"
-              << "(ThunderFFT_global) paths against hipFFT Z2Z (fp64) of the represented input.\n"
-              << "Default batch 64 (1..65536); --quick: batch 16, Gaussian input, public tail 1.\n"
-              << "Pass: finite output, relative L2 <= 0.005, unchanged LDS and output sentinels.\n"
-              << "--host-only: the 18 API argument checks, without any HIP call.\n"
-              << "CSV goes to stdout; --csv also writes a file. Exit: 0 pass, 1 failure, 2 error.\n";
+Options read_options(int argc, char** argv) {
+    Options o;
+    const auto flag = [](bool& b) { return [&b](const std::string&) { b = true; }; };
+    thff_cli::parse_options(
+        argc, argv,
+        {{"--help", false, flag(o.help)},
+         {"-h", false, flag(o.help)},
+         {"--quick", false, flag(o.quick)},
+         {"--host-only", false, flag(o.host_only)},
+         {"--device", true, [&o](const std::string& v) { o.device = int_option(v, "device"); }},
+         {"--batch", true,
+          [&o](const std::string& v) {
+              o.batch = int_option(v, "batch");
+              o.batch_set = true;
+          }},
+         {"--csv", true, [&o](const std::string& v) { o.csv = v; }}});
+    if (o.help) return o;
+    if (o.quick && !o.batch_set) o.batch = 16;
+    if (o.device < 0) throw std::runtime_error("Device must be nonnegative");
+    if (o.batch <= 0 || o.batch > 65536) throw std::runtime_error("Batch must be in 1..65536");
+    if (o.host_only && !o.csv.empty())
+        throw std::runtime_error("--csv requires GPU validation; omit it with --host-only");
+    return o;
 }
+
+const char* const kUsage =
+    " [--device N] [--batch N] [--csv PATH] [--quick] [--host-only]\n"
+    "All seven lengths, fp32/fp16, forward/inverse, direct (device API) and public\n"
+    "(ThunderFFT_global) paths against hipFFT Z2Z (fp64) of the represented input.\n"
+    "Default batch 64 (1..65536); --quick: batch 16, Gaussian input, public tail 1.\n"
+    "Pass: finite output, relative L2 <= 0.005, unchanged LDS and output sentinels.\n"
+    "--host-only: the 18 API argument checks, without any HIP call.\n"
+    "CSV goes to stdout; --csv also writes a file. Exit: 0 pass, 1 failure, 2 error.\n";
 
 }  // namespace
 
 int main(int argc, char** argv) {
     try {
-        Options o;
-        for (int i = 1; i < argc; ++i) {
-            const std::string a = argv[i];
-            if (a == "--help" || a == "-h") {
-                usage(argv[0]);
-                return 0;
-            }
-            if (a == "--quick") { o.quick = true; continue; }
-            if (a == "--host-only") { o.host_only = true; continue; }
-            if (a != "--device" && a != "--batch" && a != "--csv")
-                throw std::runtime_error("Unknown option: " + a);
-            if (++i >= argc) throw std::runtime_error("Missing value for " + a);
-            if (a == "--device") {
-                o.device = parse_int(argv[i], "device");
-            } else if (a == "--batch") {
-                o.batch = parse_int(argv[i], "batch");
-                o.batch_set = true;
-            } else {
-                o.csv = argv[i];
-            }
+        const Options o = read_options(argc, argv);
+        if (o.help) {
+            std::cout << "Usage: " << argv[0] << kUsage;
+            return 0;
         }
-        if (o.quick && !o.batch_set) o.batch = 16;
-        if (o.device < 0) throw std::runtime_error("Device must be nonnegative");
-        if (o.batch <= 0 || o.batch > 65536) throw std::runtime_error("Batch must be in 1..65536");
-        if (o.host_only && !o.csv.empty())
-            throw std::runtime_error("--csv requires GPU validation; omit it with --host-only");
-        host_checks<float>();
-        host_checks<half>();
-        std::cerr << "Host API validation: " << g_checks << " checks passed before any HIP calls\n";
-        if (g_checks != 18) return 2;
+        const int checks = run_host_checks();
+        std::cerr << "Host API validation: " << checks << " checks passed before any HIP calls\n";
         if (o.host_only) return 0;
-        hip_ok(hipSetDevice(o.device), "hipSetDevice");
+        hip_check(hipSetDevice(o.device), "hipSetDevice");
         Report rep(o.csv);
         run_type<float>(rep, o);
         run_type<half>(rep, o);

@@ -98,9 +98,34 @@ void enqueue_mfma4096(Grid g, const __half2* x, __half2* y, int batch, const flo
                                                                 g.tiles_per_block);
 }
 
+// Buffers that are element-aligned but not 16-byte aligned (any vec2_t<T>
+// pointer, the reference's contract): the VALU kernel with direct movement
+// (DirectIO, fft_tile.hpp), whose accesses are one element each, one tile
+// per workgroup.
+template <class IO, int N>
+void enqueue_unaligned(bool forward, const IO* x, IO* y, int batch, const float2* tw,
+                       hipStream_t stream) {
+    const unsigned blocks =
+        static_cast<unsigned>((static_cast<long long>(batch) + C2CPlan<N>::kFPB - 1) /
+                              C2CPlan<N>::kFPB);
+    if (forward)
+        c2c_kernel<IO, N, true, false, true><<<blocks, 256, 0, stream>>>(x, y, batch, tw, 1);
+    else
+        c2c_kernel<IO, N, false, false, true><<<blocks, 256, 0, stream>>>(x, y, batch, tw, 1);
+}
+
 template <int N>
-hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, int batch,
-                      const float2* tw, int num_cus, hipStream_t stream) {
+hipError_t launch_c2c(int precision, bool forward, bool aligned16, const void* in, void* out,
+                      int batch, const float2* tw, int num_cus, hipStream_t stream) {
+    if (!aligned16) {
+        if (precision == 0)
+            enqueue_unaligned<float2, N>(forward, static_cast<const float2*>(in),
+                                         static_cast<float2*>(out), batch, tw, stream);
+        else
+            enqueue_unaligned<__half2, N>(forward, static_cast<const __half2*>(in),
+                                          static_cast<__half2*>(out), batch, tw, stream);
+        return hipGetLastError();
+    }
     const bool mfma = precision != 0 && kHalfOnMfma<N>;
     long long fpb = C2CPlan<N>::kFPB;  // 1 for N = 4096 on either kernel
     if constexpr (kHalfOnMfma<N>)
@@ -347,8 +372,8 @@ hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y,
 }
 #endif
 
-template hipError_t launch_c2c<THFF_N>(int, bool, const void*, void*, int, const float2*, int,
-                                       hipStream_t);
+template hipError_t launch_c2c<THFF_N>(int, bool, bool, const void*, void*, int, const float2*,
+                                       int, hipStream_t);
 template hipError_t launch_conv1d<THFF_N>(int, bool, const void*, const void*, void*, int,
                                           const float2*, int, hipStream_t);
 template hipError_t launch_conv1d_real_filter<THFF_N>(const float*, float2*, int, float,

@@ -11,7 +11,7 @@
 #include <climits>
 #include <cmath>
 #include <cstdint>
-#include <map>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -40,15 +40,52 @@ bool supported_precision(int p) { return p == THFF_FLOAT || p == THFF_HALF; }
 
 const char* precision_name(int p) { return p == THFF_FLOAT ? "float" : "half"; }
 
-// One cached table per (device, precision), replaced when N changes
-// (thunderfft_impl_twiddle.cuh:26-36,310-326).
-struct CacheEntry {
-    float2* table = nullptr;
-    int n = 0;
-    int num_cus = 0;
+// Twiddle registry: one table per (precision, device) is current, as in the
+// reference cache (thunderfft_impl_twiddle.cuh:26-36,310-326).  Transforms
+// read it without a lock: `current` names the live length and `table[s]`
+// the table of length 64 << s, both published with release stores after the
+// table is filled.  Initialize with a new length makes that length current
+// and keeps the replaced table allocated (it is freed by Finalize), so a
+// transform that another thread has just enqueued never reads freed memory;
+// Initialize and Finalize are serialised per precision by g_mutex, like the
+// reference's per-T mutex.  At most the seven tables of one precision stay
+// allocated per device (8128 values, 65 KB).  Finalize while a transform that
+// uses the table is still in flight on another thread is the caller's race,
+// as in the reference.
+constexpr int kMaxDevices = 64;
+constexpr int kLengths = 7;  // 64 << s, s < 7
+
+struct DeviceTables {
+    std::atomic<int> current{0};  // live length, 0 when released
+    std::atomic<int> num_cus{0};
+    std::atomic<float2*> table[kLengths] = {};
 };
-std::map<int, CacheEntry> g_cache[2];
+DeviceTables g_tables[2][kMaxDevices];
 std::mutex g_mutex[2];
+
+int length_slot(int n) {
+    int s = 0;
+    while ((64 << s) < n) ++s;
+    return s;
+}
+
+// The current device's registry entry, or null with the error recorded.
+DeviceTables* device_tables(int precision, const char* who, int* device_out) {
+    int device = 0;
+    const hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) {
+        fail_hip(err, who);
+        return nullptr;
+    }
+    if (device < 0 || device >= kMaxDevices) {
+        fail(THFF_EIO, std::string("[ThunderFFT] ") + who + ": device " + std::to_string(device) +
+                           " is beyond the " + std::to_string(kMaxDevices) +
+                           " devices this build supports");
+        return nullptr;
+    }
+    if (device_out) *device_out = device;
+    return &g_tables[precision][device];
+}
 
 // W[m] = (cos, sin)(2*pi*m/N) in fp64, rounded once to fp32; the quarter
 // points are exact so that W[0] = 1 + 0i bit for bit.
@@ -66,18 +103,21 @@ std::vector<float2> build_table(int n) {
     return h;
 }
 
-hipError_t dispatch(int n, int precision, bool forward, const void* in, void* out, int batch,
-                    const float2* tw, int cus, hipStream_t s) {
+hipError_t dispatch(int n, int precision, bool forward, bool aligned, const void* in, void* out,
+                    int batch, const float2* tw, int cus, hipStream_t s) {
+#define THFF_C2C_CASE(L) \
+    case L: return thff::launch_c2c<L>(precision, forward, aligned, in, out, batch, tw, cus, s)
     switch (n) {
-    case 64: return thff::launch_c2c<64>(precision, forward, in, out, batch, tw, cus, s);
-    case 128: return thff::launch_c2c<128>(precision, forward, in, out, batch, tw, cus, s);
-    case 256: return thff::launch_c2c<256>(precision, forward, in, out, batch, tw, cus, s);
-    case 512: return thff::launch_c2c<512>(precision, forward, in, out, batch, tw, cus, s);
-    case 1024: return thff::launch_c2c<1024>(precision, forward, in, out, batch, tw, cus, s);
-    case 2048: return thff::launch_c2c<2048>(precision, forward, in, out, batch, tw, cus, s);
-    case 4096: return thff::launch_c2c<4096>(precision, forward, in, out, batch, tw, cus, s);
+        THFF_C2C_CASE(64);
+        THFF_C2C_CASE(128);
+        THFF_C2C_CASE(256);
+        THFF_C2C_CASE(512);
+        THFF_C2C_CASE(1024);
+        THFF_C2C_CASE(2048);
+        THFF_C2C_CASE(4096);
     default: return hipErrorInvalidValue;
     }
+#undef THFF_C2C_CASE
 }
 
 hipError_t dispatch_conv1d(int n, int precision, bool per_signal, const void* x, const void* h,
@@ -127,18 +167,18 @@ hipError_t dispatch_conv1d_real(int n, int precision, const void* x, const float
 #undef THFF_REAL_CASE
 }
 
-// The current device's cached table for (precision, n) and its CU count, or
-// an error message naming the missing ThunderFFTInitialize call.
+// The current device's table for (precision, n) and its CU count, or an
+// error naming the missing ThunderFFTInitialize call.  Lock-free: two
+// acquire loads of the registry (see DeviceTables).
 int cached_table(int precision, int n, const char* who, const float2** table, int* cus) {
     int device = 0;
-    hipError_t err = hipGetDevice(&device);
-    if (err != hipSuccess) return fail_hip(err, "hipGetDevice");
-    {
-        std::lock_guard<std::mutex> lock(g_mutex[precision]);
-        const auto found = g_cache[precision].find(device);
-        if (found != g_cache[precision].end() && found->second.n == n) {
-            *table = found->second.table;
-            *cus = found->second.num_cus;
+    DeviceTables* d = device_tables(precision, who, &device);
+    if (!d) return THFF_EIO;
+    if (d->current.load(std::memory_order_acquire) == n) {
+        const float2* t = d->table[length_slot(n)].load(std::memory_order_acquire);
+        if (t) {
+            *table = t;
+            *cus = d->num_cus.load(std::memory_order_relaxed);
             return THFF_OK;
         }
     }
@@ -314,40 +354,31 @@ int global_impl(int precision, int n, int forward, const void* d_input, void* d_
     if (batch == 0) return THFF_OK;
     if (!d_input || !d_output || d_input == d_output)
         return fail(THFF_EINVAL, "ThunderFFT requires separate non-null input/output buffers");
-    if (!aligned16(d_input) || !aligned16(d_output))
-        return fail(THFF_EINVAL, "ThunderFFT requires 16-byte aligned input/output buffers");
+    // Any vec2_t<T> buffer (the reference contract) is accepted: element
+    // alignment is required, 16-byte alignment selects the staged kernels.
+    const std::uintptr_t elem = precision == THFF_FLOAT ? 8 : 4;
+    const std::uintptr_t addr_bits = reinterpret_cast<std::uintptr_t>(d_input) |
+                                     reinterpret_cast<std::uintptr_t>(d_output);
+    if (addr_bits % elem != 0)
+        return fail(THFF_EINVAL, precision == THFF_FLOAT
+                                     ? "ThunderFFT requires 8-byte aligned float2 buffers"
+                                     : "ThunderFFT requires 4-byte aligned half2 buffers");
+    const bool aligned = addr_bits % 16 == 0;
     // The dispatch grid counts work-items in 32 bits.
     const long long fpb = thff::c2c_transforms_per_block(n);
     const long long items = (static_cast<long long>(batch) + fpb - 1) / fpb * 256;
     if (items > static_cast<long long>(UINT32_MAX))
         return fail(THFF_EINVAL, "ThunderFFT batch exceeds one launch for this length");
 
-    int device = 0;
-    hipError_t err = hipGetDevice(&device);
-    if (err != hipSuccess) return fail_hip(err, "hipGetDevice (ThunderFFT_global)");
     const float2* table = nullptr;
     int cus = 0;
-    {
-        std::lock_guard<std::mutex> lock(g_mutex[precision]);
-        const auto found = g_cache[precision].find(device);
-        if (found != g_cache[precision].end() && found->second.n == n) {
-            table = found->second.table;
-            cus = found->second.num_cus;
-        }
-    }
-    if (!table)
-        return fail(THFF_EIO, std::string("[ThunderFFT] ThunderFFT_global: no twiddle table for N=") +
-                                  std::to_string(n) + " on device " + std::to_string(device) +
-                                  "; call ThunderFFTInitialize<" + precision_name(precision) +
-                                  ">(" + std::to_string(n) + ") first");
+    const int rc = cached_table(precision, n, "ThunderFFT_global", &table, &cus);
+    if (rc != THFF_OK) return rc;
     auto s = static_cast<hipStream_t>(stream);
-    err = dispatch(n, precision, forward != 0, d_input, d_output, batch, table, cus, s);
+    hipError_t err = dispatch(n, precision, forward != 0, aligned, d_input, d_output, batch, table,
+                              cus, s);
     if (err != hipSuccess) return fail_hip(err, "ThunderFFT_global launch");
-    if (synchronize) {
-        err = hipStreamSynchronize(s);
-        if (err != hipSuccess) return fail_hip(err, "ThunderFFT_global synchronize");
-    }
-    return THFF_OK;
+    return finish(s, synchronize, "ThunderFFT_global synchronize");
 }
 
 }  // namespace
@@ -369,31 +400,27 @@ int thff_initialize(int precision, int n) {
         return fail(THFF_EINVAL, "ThunderFFTInitialize<T>: unsupported FFT size");
     std::lock_guard<std::mutex> lock(g_mutex[precision]);
     int device = 0;
-    hipError_t err = hipGetDevice(&device);
-    if (err != hipSuccess) return fail_hip(err, "hipGetDevice (initialize)");
-    CacheEntry& entry = g_cache[precision][device];
-    if (entry.table && entry.n == n) return THFF_OK;
-    if (entry.table) {
-        entry.n = 0;
-        err = hipFree(entry.table);
-        entry.table = nullptr;
-        if (err != hipSuccess) return fail_hip(err, "hipFree cached twiddle (initialize)");
+    DeviceTables* d = device_tables(precision, "hipGetDevice (initialize)", &device);
+    if (!d) return THFF_EIO;
+    if (d->current.load(std::memory_order_relaxed) == n) return THFF_OK;
+    std::atomic<float2*>& slot = d->table[length_slot(n)];
+    if (!slot.load(std::memory_order_relaxed)) {
+        int cus = 0;
+        hipError_t err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+        if (err != hipSuccess) return fail_hip(err, "hipDeviceGetAttribute (initialize)");
+        const std::vector<float2> host = build_table(n);
+        float2* table = nullptr;
+        err = hipMalloc(reinterpret_cast<void**>(&table), sizeof(float2) * n);
+        if (err != hipSuccess) return fail_hip(err, "hipMalloc twiddle table");
+        err = hipMemcpy(table, host.data(), sizeof(float2) * n, hipMemcpyHostToDevice);
+        if (err != hipSuccess) {
+            (void)hipFree(table);
+            return fail_hip(err, "hipMemcpy twiddle table");
+        }
+        d->num_cus.store(cus, std::memory_order_relaxed);
+        slot.store(table, std::memory_order_release);
     }
-    int cus = 0;
-    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
-    if (err != hipSuccess) return fail_hip(err, "hipDeviceGetAttribute (initialize)");
-    const std::vector<float2> host = build_table(n);
-    float2* table = nullptr;
-    err = hipMalloc(reinterpret_cast<void**>(&table), sizeof(float2) * n);
-    if (err != hipSuccess) return fail_hip(err, "hipMalloc twiddle table");
-    err = hipMemcpy(table, host.data(), sizeof(float2) * n, hipMemcpyHostToDevice);
-    if (err != hipSuccess) {
-        (void)hipFree(table);
-        return fail_hip(err, "hipMemcpy twiddle table");
-    }
-    entry.table = table;
-    entry.n = n;
-    entry.num_cus = cus;
+    d->current.store(n, std::memory_order_release);
     return THFF_OK;
 }
 
@@ -401,18 +428,17 @@ int thff_finalize(int precision) {
     if (!supported_precision(precision))
         return fail(THFF_EINVAL, "ThunderFFTFinalize<T>: supported T are float and half only");
     std::lock_guard<std::mutex> lock(g_mutex[precision]);
-    int device = 0;
-    hipError_t err = hipGetDevice(&device);
-    if (err != hipSuccess) return fail_hip(err, "hipGetDevice (finalize)");
-    const auto found = g_cache[precision].find(device);
-    if (found == g_cache[precision].end()) return THFF_OK;
-    float2* table = found->second.table;
-    g_cache[precision].erase(found);
-    if (table) {
-        err = hipFree(table);
-        if (err != hipSuccess) return fail_hip(err, "hipFree cached twiddle (finalize)");
+    DeviceTables* d = device_tables(precision, "hipGetDevice (finalize)", nullptr);
+    if (!d) return THFF_EIO;
+    d->current.store(0, std::memory_order_release);
+    hipError_t first = hipSuccess;
+    for (auto& slot : d->table) {
+        float2* table = slot.exchange(nullptr, std::memory_order_acq_rel);
+        if (!table) continue;
+        const hipError_t err = hipFree(table);
+        if (first == hipSuccess) first = err;
     }
-    return THFF_OK;
+    return first == hipSuccess ? THFF_OK : fail_hip(first, "hipFree cached twiddle (finalize)");
 }
 
 int thff_global(int precision, int n, int forward, const void* d_input, void* d_output, int batch,
@@ -482,12 +508,11 @@ int thff_twiddle_info(int precision, const void** d_table, int* n) {
     if (!supported_precision(precision)) return fail(THFF_EINVAL, "unsupported precision");
     if (!d_table || !n) return fail(THFF_EINVAL, "thff_twiddle_info: null output pointer");
     std::lock_guard<std::mutex> lock(g_mutex[precision]);
-    int device = 0;
-    hipError_t err = hipGetDevice(&device);
-    if (err != hipSuccess) return fail_hip(err, "hipGetDevice (twiddle info)");
-    const auto found = g_cache[precision].find(device);
-    *d_table = found == g_cache[precision].end() ? nullptr : found->second.table;
-    *n = found == g_cache[precision].end() ? 0 : found->second.n;
+    DeviceTables* d = device_tables(precision, "hipGetDevice (twiddle info)", nullptr);
+    if (!d) return THFF_EIO;
+    const int live = d->current.load(std::memory_order_acquire);
+    *n = live;
+    *d_table = live ? d->table[length_slot(live)].load(std::memory_order_acquire) : nullptr;
     return THFF_OK;
 }
 

@@ -7,11 +7,13 @@
 namespace thff {
 
 // Enqueue the batched C2C kernel for length N.  precision: 0 float2, 1 half2.
-// tw: the device's fp32 table of N values (cos, sin)(2*pi*m/N); num_cus: the
+// aligned16: both buffers start on a 16-byte boundary (otherwise they need
+// only the element's alignment, and tiles move value by value).  tw: the
+// device's fp32 table of N values (cos, sin)(2*pi*m/N); num_cus: the
 // device's compute-unit count (sizes the grid).
 template <int N>
-hipError_t launch_c2c(int precision, bool forward, const void* in, void* out, int batch,
-                      const float2* tw, int num_cus, hipStream_t stream);
+hipError_t launch_c2c(int precision, bool forward, bool aligned16, const void* in, void* out,
+                      int batch, const float2* tw, int num_cus, hipStream_t stream);
 
 // Enqueue the fused circular convolution of `batch` signals of length N:
 // y[b] = IFFT(FFT(x[b]) * FFT(h[per_signal_filter ? b : 0])) / N.
