@@ -8,6 +8,13 @@
 // stage 1 wants it) at inputs j = q + 4 r: the inverse's stage 1 consumes the
 // product straight from registers with column-permuted operands
 // (dft16_operands<..., true>), so the spectra never leave registers.
+//
+// Every transform here runs forward: the inverse of a product P is computed
+// as conj(DFT(conj(P))), with the conjugation folded into the f16 packing on
+// the way into the inverse's stage 1 and on the way out.  So one set of
+// operands and twiddles serves all three transforms, and the W_16C^(n m)
+// twiddle before the last DFT16 is folded into that stage's operands
+// (Stage3Folded, fft_mfma.hpp).
 #pragma once
 
 #include "fft_conv.hpp"
@@ -61,16 +68,16 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
     constexpr int kB = P::kBlocks;
     __shared__ unsigned lds[4 * P::kRegion];
     __shared__ cpx w1[P::kTw1];
+    __shared__ u32x4 a3[P::kA3];
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int n = lane & 15, q = lane >> 4;
     unsigned* region = lds + wave * P::kRegion;
 
-    f16x8 a[2], ai[2], ai_regs[2];
-    cpx w2[C > 1 ? C - 1 : 1];
-    mfma_setup<C, true>(a, w1, w2, tw);  // forward operands and twiddles
-    dft16_operands<false>(ai, lane);
-    dft16_operands<false, true>(ai_regs, lane);
+    f16x8 a[2], a_regs[2];
+    mfma_setup<C, true>(a, w1, a3, nullptr, tw);  // forward operands and twiddles
+    dft16_operands<true, true>(a_regs, lane);
+    const Stage3Folded s3{a, a3, lane};
 
     const long long pairs = (static_cast<long long>(batch) + 1) / 2;
     const long long transforms = pairs * channels;
@@ -117,7 +124,7 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
 
         cpx v[kB][4];
         mfma_stage1_lds<C>(region, a, lane, v);
-        mfma_steps2to6<C, true>(region, a, w1, w2, lane, v);
+        mfma_steps2to6<C, true>(region, w1, s3, lane, v);
         // ---- product: block (f, m), lane (n, q): bin k = n + 16 m + 16C (q + 4 r) ----
         // The spectra of the wave's transforms stay in registers while their
         // channels do not change: they are chan[0] + f mod D, so chan[0]
@@ -140,17 +147,17 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
         for (int b = 0; b < kB; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], spec[b][r]);
-        // ---- inverse, stage 1 straight from the registers ----
-        mfma_stage1_regs<C>(ai_regs, v);
-        mfma_steps2to6<C, false, true>(region, ai, w1, w2, lane, v);
-        // ---- real part -> row 2p, imaginary part -> row 2p + 1 ----
+        // ---- inverse = conj(DFT(conj(product))), stage 1 straight from the registers ----
+        mfma_stage1_regs<C, true>(a_regs, v);
+        mfma_steps2to6<C, true>(region, w1, s3, lane, v);
+        // ---- real part -> row 2p, imaginary part -> row 2p + 1 (conjugated back) ----
         wave_lds_sync();
 #pragma unroll
         for (int b = 0; b < kB; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
                 region[P::out_pad((b / C) * N + n + 16 * (b % C) + P::kM * (q + 4 * r))] =
-                    pack_half2(v[b][r]);
+                    pack_half2({v[b][r].re, -v[b][r].im});
         wave_lds_sync();
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -187,17 +194,20 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
     constexpr int kRaw = P::kVals / 4;  // 16-byte loads per lane
     __shared__ unsigned lds[4 * P::kRegion];
     __shared__ cpx w1[P::kTw1];
+    __shared__ u32x4 a3[P::kA3];
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int n = lane & 15, q = lane >> 4;
     unsigned* region = lds + wave * P::kRegion;
-    constexpr float kScale = 1.0f / N;
 
-    f16x8 a[2], ai[2], ai_regs[2];
-    cpx w2[C > 1 ? C - 1 : 1];
-    mfma_setup<C, true>(a, w1, w2, tw);
-    dft16_operands<false>(ai, lane);
-    dft16_operands<false, true>(ai_regs, lane);
+    f16x8 a[2], a_regs[2];
+    mfma_setup<C, true>(a, w1, a3, nullptr, tw);
+    // The inverse's stage-1 operands carry the 1/N of the convolution: a
+    // power of two, exact in f16 for every coefficient here (|c| >= 0.38).
+    dft16_operands<true, true>(a_regs, lane);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) a_regs[h] *= static_cast<_Float16>(1.0f / N);
+    const Stage3Folded s3{a, a3, lane};
 
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
     long long tile, tile_end, step;
@@ -222,15 +232,15 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
             *reinterpret_cast<u32x4*>(region + P::in_pad(4 * lane + 256 * i)) = raw[i];
         wave_lds_sync();
         mfma_stage1_lds<C>(region, a, lane, v);
-        mfma_steps2to6<C, true>(region, a, w1, w2, lane, v);
+        mfma_steps2to6<C, true>(region, w1, s3, lane, v);
     };
 
-    unsigned hp[kB][4];  // FFT(h) / N, packed half2
+    unsigned hp[kB][4];  // FFT(h), packed half2
     auto keep = [&](const cpx (&v)[kB][4]) {
 #pragma unroll
         for (int b = 0; b < kB; ++b)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) hp[b][r] = pack_half2({v[b][r].re * kScale, v[b][r].im * kScale});
+            for (int r = 0; r < 4; ++r) hp[b][r] = pack_half2(v[b][r]);
     };
     if constexpr (!kPerSignal) {
         // Every transform of the wave is the shared filter: stage it kFPW times.
@@ -244,7 +254,7 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
         }
         wave_lds_sync();
         mfma_stage1_lds<C>(region, a, lane, v);
-        mfma_steps2to6<C, true>(region, a, w1, w2, lane, v);
+        mfma_steps2to6<C, true>(region, w1, s3, lane, v);
         keep(v);
     }
 
@@ -264,8 +274,9 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
                 const float2 hk = __half22float2(__builtin_bit_cast(__half2, hp[b][r]));
                 v[b][r] = cmul(v[b][r], cpx{hk.x, hk.y});
             }
-        mfma_stage1_regs<C>(ai_regs, v);
-        mfma_steps2to6<C, false, true>(region, ai, w1, w2, lane, v);
+        // ---- inverse = conj(DFT(conj(product))) / N, stage 1 from the registers ----
+        mfma_stage1_regs<C, true>(a_regs, v);
+        mfma_steps2to6<C, true>(region, w1, s3, lane, v);
         // ---- store: block (f, m), lane (n, q) holds y_f[n + 16 m + 16C (q + 4 r)] ----
         wave_lds_sync();
 #pragma unroll
@@ -273,7 +284,7 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
 #pragma unroll
             for (int r = 0; r < 4; ++r)
                 region[P::out_pad((b / C) * N + n + 16 * (b % C) + P::kM * (q + 4 * r))] =
-                    pack_half2(v[b][r]);
+                    pack_half2({v[b][r].re, -v[b][r].im});
         wave_lds_sync();
         __half2* dst = y + off;
 #pragma unroll

@@ -121,19 +121,93 @@ struct MfmaPlan {
     static constexpr int kOutSize = kWaveVals + kOutPad * (kWaveVals / kOutPeriod);
     static constexpr int kRegion = kInSize > kOutSize ? kInSize : kOutSize;  // dwords per wave
     static constexpr int kTw1 = C * 4 * 64;        // first twiddles, [c][r][lane]
+    static constexpr int kA3 = (C > 1 ? C - 1 : 1) * 2 * 64;  // folded stage-3 operands (u32x4)
     __device__ static __forceinline__ int in_pad(int k) { return k + kInPad * (k / kInPeriod); }
     __device__ static __forceinline__ int out_pad(int k) {
         return k + kOutPad * (k / kOutPeriod);
     }
 };
 
-// Per-lane DFT16 operands, the step-2 twiddles W_N^(t*k1) (t = 16c + n,
-// k1 = q + 4r; shared by the workgroup through LDS, w1 = [c][r][lane]) and the
-// step-4 twiddles W_16C^(n*m) = W_N^(16 n m) (registers), all from the
-// positive-angle table and conjugated here for the forward direction.
-// Collective over the 256-lane workgroup (ends with a barrier).
+// Half h of this lane's DFT16 A operand built from the positive-angle table
+// tw of length N = 256 C, with input (column) j of the matrix scaled by
+// W_16C^(j m): entry (k, j) is W_16^(j k) W_16C^(j m) = W_N^(16 j (k C + m)).
+// m = 0 gives the plain DFT16 matrix (the table's values at multiples of N/16
+// are the correctly rounded cos/sin, as the constants of dft16_operands).
+// Row and column order as dft16_operands<FWD, false>.
+template <bool FWD>
+__device__ __forceinline__ f16x8 dft16_operand_twiddled(int lane, int h, int m, int C,
+                                                        const float2* __restrict__ tw) {
+    const int N = 256 * C;
+    const int mr = lane & 15, q = lane >> 4;
+    const int k = (mr >> 2) + 4 * (2 * h + ((mr & 3) >> 1));
+    const int o = mr & 1;
+    f16x8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int kk = 8 * q + e;
+        const int j = kk >> 1, p = kk & 1;
+        const float2 w = tw[(16 * j * (k * C + m)) & (N - 1)];
+        const float c = w.x, sn = FWD ? -w.y : w.y;
+        // out.re = c*in.re - s*in.im ; out.im = s*in.re + c*in.im
+        const float v = o == 0 ? (p == 0 ? c : -sn) : (p == 0 ? sn : c);
+        r[e] = static_cast<_Float16>(v);
+    }
+    return r;
+}
+
+// Where steps 5-6 take the DFT16 operands of block column m (the DFT16 over n
+// of the sequences (k1, m)) and how the twiddle W_16C^(n m) between the
+// DFT_C and that DFT16 is applied.
+//
+// Stage3Folded: the twiddle is folded into the operands.  Column n of block
+// column m's matrix is scaled by W_16C^(n m) (dft16_operand_twiddled), so no
+// multiply remains between the DFT_C and the transpose; m = 0 uses the plain
+// operands `a`, m >= 1 read theirs from the workgroup's LDS table
+// a3[m - 1][half][lane] (mfma_setup).  The factor is rounded into the f16
+// coefficient, the size of the f16 rounding of the data at that stage.
+struct Stage3Folded {
+    static constexpr bool kTwiddle = false;
+    const f16x8* a;   // a[2]: plain operands
+    const u32x4* a3;  // [(m - 1) * 2 + half] * 64 + lane
+    int lane;
+    __device__ __forceinline__ cpx twiddle(int, cpx v) const { return v; }
+    __device__ __forceinline__ void operands(int m, f16x8 (&op)[2]) const {
+        if (m == 0) {
+            op[0] = a[0];
+            op[1] = a[1];
+        } else {
+            op[0] = __builtin_bit_cast(f16x8, a3[((m - 1) * 2) * 64 + lane]);
+            op[1] = __builtin_bit_cast(f16x8, a3[((m - 1) * 2 + 1) * 64 + lane]);
+        }
+    }
+};
+
+// Stage3Plain: plain operands for every block column and the fp32 twiddles
+// w2[m - 1] = W_16C^(n m) in registers (conjugated at use with kConj), for
+// callers without the workgroup set-up (the device-side API).
+template <bool kConj>
+struct Stage3Plain {
+    static constexpr bool kTwiddle = true;
+    const f16x8* a;
+    const cpx* w2;
+    __device__ __forceinline__ cpx twiddle(int m, cpx v) const {
+        return kConj ? cmulc(v, w2[m - 1]) : cmul(v, w2[m - 1]);
+    }
+    __device__ __forceinline__ void operands(int, f16x8 (&op)[2]) const {
+        op[0] = a[0];
+        op[1] = a[1];
+    }
+};
+
+// Workgroup set-up of the MFMA kernels for direction FWD, from the
+// positive-angle table: this lane's plain DFT16 operands, the step-2 twiddles
+// W_N^(t*k1) (t = 16c + n, k1 = q + 4r) shared through LDS as
+// w1 = [c][r][lane], and for the stage before the last DFT16 either the
+// folded operands a3 (Stage3Folded; a3 non-null) or this lane's twiddles
+// w2[m - 1] = W_16C^(n m) (Stage3Plain; w2 non-null).  Collective over the
+// 256-lane workgroup (ends with a barrier).
 template <int C, bool FWD>
-__device__ __forceinline__ void mfma_setup(f16x8 (&a)[2], cpx* w1, cpx* w2,
+__device__ __forceinline__ void mfma_setup(f16x8 (&a)[2], cpx* w1, u32x4* a3, cpx* w2,
                                            const float2* __restrict__ tw) {
     using P = MfmaPlan<C>;
     constexpr int N = P::N;
@@ -144,10 +218,20 @@ __device__ __forceinline__ void mfma_setup(f16x8 (&a)[2], cpx* w1, cpx* w2,
         const float2 x = tw[((16 * c + (l & 15)) * ((l >> 4) + 4 * r)) & (N - 1)];
         w1[e] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
     }
+    if constexpr (C > 1) {
+        if (a3) {
+            for (int e = tid; e < (C - 1) * 2 * 64; e += 256) {
+                const int l = e & 63, h = (e >> 6) & 1, m = 1 + (e >> 7);
+                a3[e] = __builtin_bit_cast(u32x4, dft16_operand_twiddled<FWD>(l, h, m, C, tw));
+            }
+        }
+        if (w2) {
 #pragma unroll
-    for (int m = 1; m < C; ++m) {
-        const float2 x = tw[(16 * n * m) & (N - 1)];
-        w2[m - 1] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+            for (int m = 1; m < C; ++m) {
+                const float2 x = tw[(16 * n * m) & (N - 1)];
+                w2[m - 1] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+            }
+        }
     }
     __syncthreads();
 }
@@ -171,29 +255,29 @@ __device__ __forceinline__ void mfma_stage1_lds(const unsigned* region, const f1
 }
 
 // Step 1 from registers: y[b][r] holds z_f[16 c + n + 16C (q + 4 r)] (the
-// layout a forward transform leaves), `a` built with kInterleaved.
-template <int C>
+// layout a forward transform leaves), `a` built with kInterleaved.  With
+// kConj the inputs are conjugated on the way in (folded into the f16 pack).
+template <int C, bool kConj = false>
 __device__ __forceinline__ void mfma_stage1_regs(const f16x8 (&a)[2],
                                                  cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
 #pragma unroll
     for (int b = 0; b < MfmaPlan<C>::kBlocks; ++b) {
         u32x4 x;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) x[r] = pack_half2(y[b][r]);
+        for (int r = 0; r < 4; ++r)
+            x[r] = pack_half2(kConj ? cpx{y[b][r].re, -y[b][r].im} : y[b][r]);
         dft16_block(a, as_f16x8(x), y[b]);
     }
 }
 
-// Steps 2-6 on the stage-1 outputs: twiddle, DFT_C over c, twiddle, LDS
-// transpose through `region` (overwritten), DFT16 over n.  The twiddle
-// tables hold the direction TW_FWD (w1 = [c][r][lane] in LDS, w2 in
-// registers); a transform of the other direction uses their conjugates.
-// On return lane (n = k1, q) holds, for block b = (f, m),
-// y[b][r] = X_f[k1 + 16 m + 16C (q + 4 r)].
+// Steps 2-6 on the stage-1 outputs: twiddle, DFT_C over c, twiddle (S3),
+// LDS transpose through `region` (overwritten), DFT16 over n with S3's
+// operands.  The step-2 twiddles hold the direction TW_FWD; a transform of
+// the other direction uses their conjugates.  On return lane (n = k1, q)
+// holds, for block b = (f, m), y[b][r] = X_f[k1 + 16 m + 16C (q + 4 r)].
 // `w1(c, r)` returns this lane's step-2 twiddle of block column c, output r.
-template <int C, bool FWD, bool TW_FWD = FWD, class W1>
-__device__ __forceinline__ void mfma_steps2to6_w(unsigned* region, const f16x8 (&a)[2], W1 w1,
-                                                 const cpx* w2, int lane,
+template <int C, bool FWD, bool TW_FWD = FWD, class W1, class S3>
+__device__ __forceinline__ void mfma_steps2to6_w(unsigned* region, W1 w1, const S3& s3, int lane,
                                                  cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
     using P = MfmaPlan<C>;
     constexpr int kB = P::kBlocks;
@@ -213,7 +297,7 @@ __device__ __forceinline__ void mfma_steps2to6_w(unsigned* region, const f16x8 (
             Dft<C, FWD>::run(v);
             y[f * C][r] = v[0];
 #pragma unroll
-            for (int m = 1; m < C; ++m) y[f * C + m][r] = kConj ? cmulc(v[m], w2[m - 1]) : cmul(v[m], w2[m - 1]);
+            for (int m = 1; m < C; ++m) y[f * C + m][r] = S3::kTwiddle ? s3.twiddle(m, v[m]) : v[m];
         }
     // ---- step 5: transpose: row 16b + k1 holds the 16 inputs n of
     // sequence (k1, m) of block b = (f, m); its 4-value chunks are rotated
@@ -232,26 +316,28 @@ __device__ __forceinline__ void mfma_steps2to6_w(unsigned* region, const f16x8 (
     for (int b = 0; b < kB; ++b) {
         const u32x4 x = *reinterpret_cast<const u32x4*>(
             region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
-        dft16_block(a, as_f16x8(x), y[b]);
+        f16x8 op[2];
+        s3.operands(b % C, op);
+        dft16_block(op, as_f16x8(x), y[b]);
     }
 }
 
 // Steps 2-6 with the step-2 twiddles in the workgroup's LDS table w1 = [c][r][lane].
-template <int C, bool FWD, bool TW_FWD = FWD>
-__device__ __forceinline__ void mfma_steps2to6(unsigned* region, const f16x8 (&a)[2],
-                                               const cpx* w1, const cpx* w2, int lane,
-                                               cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
+template <int C, bool FWD, bool TW_FWD = FWD, class S3>
+__device__ __forceinline__ void mfma_steps2to6(unsigned* region, const cpx* w1, const S3& s3,
+                                               int lane, cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
     mfma_steps2to6_w<C, FWD, TW_FWD>(
-        region, a, [&](int c, int r) { return w1[(c * 4 + r) * 64 + lane]; }, w2, lane, y);
+        region, [&](int c, int r) { return w1[(c * 4 + r) * 64 + lane]; }, s3, lane, y);
 }
 
-// Steps 1-6 for the kFPW transforms a wave has staged in `region`.
-template <int C, bool FWD>
+// Steps 1-6 for the kFPW transforms a wave has staged in `region`, with the
+// workgroup set-up of mfma_setup and the stage-3 form S3.
+template <int C, bool FWD, class S3>
 __device__ __forceinline__ void mfma_fft_staged(unsigned* region, const f16x8 (&a)[2],
-                                                const cpx* w1, const cpx* w2, int lane,
+                                                const cpx* w1, const S3& s3, int lane,
                                                 cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
     mfma_stage1_lds<C>(region, a, lane, y);
-    mfma_steps2to6<C, FWD>(region, a, w1, w2, lane, y);
+    mfma_steps2to6<C, FWD>(region, w1, s3, lane, y);
 }
 
 // One MFMA transform of the kFPW transforms a wave holds in registers, for
@@ -286,7 +372,7 @@ __device__ __forceinline__ void mfma_fft_regs(unsigned* region, const float2* __
     }
     mfma_stage1_regs<C>(a_in, y);
     mfma_steps2to6_w<C, FWD>(
-        region, a, [&](int c, int r) { return w1[c * 4 + r]; }, w2, lane, y);
+        region, [&](int c, int r) { return w1[c * 4 + r]; }, Stage3Plain<false>{a, w2}, lane, y);
 }
 
 // Batched C2C of half2 signals of N = 256*C on MFMA (C = 4 is N = 1024 as
@@ -318,9 +404,13 @@ c2c_mfma_kernel(const __half2* __restrict__ in,
     const int n = lane & 15, q = lane >> 4;
     unsigned* region = lds + wave * P::kRegion;
 
+    // The twiddle before the last DFT16 stays an fp32 multiply here: folding
+    // it into LDS-held operands (as the convolutions do) measured slower for
+    // the transform alone (compute pass 29.8 vs 27.8 us at N = 1024).
     f16x8 a[2];
     cpx w2[C > 1 ? C - 1 : 1];
-    mfma_setup<C, FWD>(a, w1, w2, tw);
+    mfma_setup<C, FWD>(a, w1, nullptr, w2, tw);
+    const Stage3Plain<false> s3{a, w2};
 
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
     long long tile, tile_end, step;
@@ -362,7 +452,7 @@ c2c_mfma_kernel(const __half2* __restrict__ in,
         wave_lds_sync();
 
         cpx y[kB][4];
-        mfma_fft_staged<C, FWD>(region, a, w1, w2, lane, y);
+        mfma_fft_staged<C, FWD>(region, a, w1, s3, lane, y);
         // ---- store: lane (n = k1, q), block (f, m) holds X_f[k1 + 16 m + 16C (q + 4 r)] ----
         wave_lds_sync();
 #pragma unroll

@@ -47,7 +47,8 @@ __global__ __launch_bounds__(256) void repeat_mfma(const __half2* in, __half2* o
     unsigned* region = lds + wave * P::kRegion;
     f16x8 a[2];
     cpx w2[C > 1 ? C - 1 : 1];
-    mfma_setup<C, true>(a, w1, w2, tw);
+    mfma_setup<C, true>(a, w1, nullptr, w2, tw);
+    const Stage3Plain<false> s3{a, w2};
     const long long first = static_cast<long long>(blockIdx.x) * P::kFPB + wave * P::kFPW;
     const bool valid = first + P::kFPW <= batch;
     const __half2* src = in + first * N;
@@ -59,7 +60,7 @@ __global__ __launch_bounds__(256) void repeat_mfma(const __half2* in, __half2* o
 #pragma unroll 1
     for (int i = 0; i < repeats; ++i) {
         wave_lds_sync();
-        mfma_fft_staged<C, true>(region, a, w1, w2, lane, y);
+        mfma_fft_staged<C, true>(region, a, w1, s3, lane, y);
         wave_lds_sync();
 #pragma unroll
         for (int b = 0; b < P::kBlocks; ++b)
