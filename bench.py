@@ -61,6 +61,9 @@ def parse():
     ap.add_argument("--settle-ms", type=float, default=60.0,
                     help="per leg, after its W warm-up launches: further untimed launches of "
                          "that leg's kernel filling about this many ms before the timed ones")
+    ap.add_argument("--compute", action="store_true",
+                    help="only the differential-compute legs (every kernel of "
+                         "COMPUTE_MODES); prints one JSON line")
     ap.add_argument("--sweep", action="store_true",
                     help="the size sweep instead: every N at batch 2^26/N, both types and "
                          "directions; prints one line per case and a JSON summary")
@@ -284,6 +287,19 @@ def time_conv_valid(T: str, ntaps: int, steps: int, warmup: int) -> dict:
             "bytes_per_call": nbytes}
 
 
+# Differential-compute kernels of libthff_bench_compute.so (thffx_compute_repeat's
+# precision argument): the library's float and half transforms, and the float
+# transform with both DFT16 stages on the matrix cores (exact fp32 MFMA, and a
+# bf16x3 split), the measurement of the float path on MFMA.
+COMPUTE_MODES = {"float": 0, "half": 1, "float_mfma_f32": 2, "float_mfma_bf16x3": 3}
+COMPUTE_KERNELS = {
+    "float": "fp32 VALU passes (the library's float kernel)",
+    "half": "fp16 MFMA (v_mfma_f32_16x16x32_f16)",
+    "float_mfma_f32": "fp32 data, both DFT16 stages on v_mfma_f32_16x16x4_f32",
+    "float_mfma_bf16x3": "fp32 data, both DFT16 stages as bf16x3 on v_mfma_f32_16x16x32_bf16",
+}
+
+
 def compute_differential(T: str, repeats: int = 1000, trials: int = 3) -> dict:
     """Reference-style compute time of the N=1024, batch-65536 transform
     (sample/bench/paper_fft.cu:131-148): one launch loads every tile once,
@@ -301,14 +317,15 @@ def compute_differential(T: str, repeats: int = 1000, trials: int = 3) -> dict:
     L.thffx_compute_repeat.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
                                        ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     n, batch = N_FFT, BATCH
-    dt = torch.float32 if T == "float" else torch.float16
+    storage = "half" if T == "half" else "float"
+    dt = torch.float32 if storage == "float" else torch.float16
     x = torch.empty(2 * n * batch, dtype=dt, device="cuda")
     y = torch.empty_like(x)
     stream = torch.cuda.current_stream()
-    thff.fill_uniform(T, x, n * batch, 0x7F4A7C15 + n, 0, stream)
+    thff.fill_uniform(storage, x, n * batch, 0x7F4A7C15 + n, 0, stream)
     x.mul_(1.0 / 32.0)  # keeps the repeated values finite a little longer
-    thff.ThunderFFTInitialize(T, n)
-    prec = 0 if T == "float" else 1
+    thff.ThunderFFTInitialize(storage, n)
+    prec = COMPUTE_MODES[T]
 
     def once(r):
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -326,13 +343,12 @@ def compute_differential(T: str, repeats: int = 1000, trials: int = 3) -> dict:
     for _ in range(trials):
         t_r, t_2r = once(repeats), once(2 * repeats)
         per.append((t_2r - t_r) / repeats)
-    thff.ThunderFFTFinalize(T)
+    thff.ThunderFFTFinalize(storage)
     del x, y
     per.sort()
     return {"precision": T, "repeats": repeats, "trials": trials,
-            "compute_us_per_pass": per[len(per) // 2],
-            "kernel": "fp32 VALU passes" if T == "float" else "fp16 MFMA (v_mfma_f32_16x16x32_f16)",
-            "reference_a100_us": 126.53 if T == "float" else None}
+            "compute_us_per_pass": per[len(per) // 2], "kernel": COMPUTE_KERNELS[T],
+            "reference_a100_us": 126.53 if storage == "float" else None}
 
 
 def copy_bandwidth(steps: int, warmup: int) -> tuple[float, float]:
@@ -446,7 +462,8 @@ def sync_wrapper(T: str, calls: int = 25, warmup: int = 10) -> dict:
 
 
 def host_fp64_check(subset: int = 256) -> dict:
-    """The host fp64 check, timed on its own: the GPU's float forward transform
+    """Part of the cpu_baseline leg (the oracle runs only there, as the
+    checker).  The host fp64 check, timed on its own: the GPU's float forward transform
     of the bench input (N=1024, batch 65536) against the oracle's fp64 radix-2
     FFT of the same seeded input over the full batch (one thread), and that
     FFT against the fp64 direct DFT on a `subset`-signal subset."""
@@ -585,6 +602,15 @@ def main():
     if a.sweep:
         sweep(a)
         return
+    if a.compute:
+        out = {}
+        for T in COMPUTE_MODES:
+            r = compute_differential(T)
+            out[T] = {k: (sig(v) if isinstance(v, float) else v) for k, v in r.items()}
+            print(f"[compute] {T} ({r['kernel']}): {r['compute_us_per_pass']:.1f} us per pass",
+                  file=sys.stderr, flush=True)
+        print(json.dumps({"compute": out}), flush=True)
+        return
     runs = {}
     for T in ("float", "half"):
         for fwd in (True, False):
@@ -613,11 +639,12 @@ def main():
         print(f"[bench] {r['workload']}: {r['us_per_call']:.1f} us, {r['gbps']:.0f} GB/s "
               f"({r['pct_hbm_peak']:.1f}% of HBM peak), {r['gflops']:.0f} GFLOP/s",
               file=sys.stderr, flush=True)
-    for T in ("float", "half"):
+    for T in COMPUTE_MODES:
         r = compute_differential(T)
         runs[f"compute_{T}"] = r
-        print(f"[bench] {T} N=1024 x 65536 differential compute (R={r['repeats']}): "
-              f"{r['compute_us_per_pass']:.1f} us per pass", file=sys.stderr, flush=True)
+        print(f"[bench] {T} N=1024 x 65536 differential compute (R={r['repeats']}, "
+              f"{r['kernel']}): {r['compute_us_per_pass']:.1f} us per pass",
+              file=sys.stderr, flush=True)
     for T in ("float", "half"):
         r = sync_wrapper(T)
         runs[f"sync_wrapper_{T}_fwd"] = r
@@ -631,14 +658,17 @@ def main():
           f"({100.0 * copy_gbps / HBM_PEAK_GBPS:.1f}% of HBM peak); torch copy_ {torch_copy_gbps:.0f} GB/s",
           file=sys.stderr, flush=True)
     main_run = runs["float_fwd"]
-    fp64 = None
-    if not a.no_fp64_check:
-        fp64 = host_fp64_check()
-        print(f"[bench] host fp64 check: fp64 FFT of {fp64['fp64_fft_signals']} signals "
-              f"{fp64['fp64_fft_s']:.1f} s, direct DFT of {fp64['direct_dft_signals']} "
-              f"{fp64['direct_dft_s']:.2f} s; GPU float forward vs fp64 rel L2 "
-              f"{fp64['gpu_float_fwd_vs_fp64_rel_l2']:.3e}", file=sys.stderr, flush=True)
-    cpu = None if a.no_cpu else cpu_baseline(a.cpu_seconds)
+    cpu = None
+    if not a.no_cpu:
+        cpu = cpu_baseline(a.cpu_seconds)
+        if not a.no_fp64_check:
+            fp64 = host_fp64_check()
+            print(f"[bench] host fp64 check: fp64 FFT of {fp64['fp64_fft_signals']} signals "
+                  f"{fp64['fp64_fft_s']:.1f} s, direct DFT of {fp64['direct_dft_signals']} "
+                  f"{fp64['direct_dft_s']:.2f} s; GPU float forward vs fp64 rel L2 "
+                  f"{fp64['gpu_float_fwd_vs_fp64_rel_l2']:.3e}", file=sys.stderr, flush=True)
+            cpu["host_fp64_check"] = {k: (sig(v) if isinstance(v, float) else v)
+                                      for k, v in fp64.items()}
     achieved = main_run["gbps"]
     out = {
         "metric": "C2C FFT µs, GFLOP/s and % HBM peak at N=1024 b=65536 (fp32/fp16)",
@@ -672,8 +702,6 @@ def main():
                      "kernel": "thff::c2c_kernel<float2, 1024, true, false, false>",
                      "algorithmic_bytes": main_run["bytes_per_call"]},
         "cpu_baseline": cpu,
-        "host_fp64_check": ({k: (sig(v) if isinstance(v, float) else v) for k, v in fp64.items()}
-                            if fp64 else None),
         "median_us_per_call": sig(main_run["median_us_per_call"]),
         "also": {k: {kk: (sig(vv) if isinstance(vv, float) else vv)
                      for kk, vv in v.items()} for k, v in runs.items()},
