@@ -253,7 +253,9 @@ def time_conv_real(T: str, n: int, steps: int, warmup: int) -> dict:
 def time_conv_valid(T: str, ntaps: int, steps: int, warmup: int) -> dict:
     """The reference's tiled valid conv1d (sample/conv1d/main.cu:38-174) on one
     complex signal of 2^26 samples with `ntaps` complex taps (its default is
-    9), 64-point FFT windows with 65 - ntaps valid outputs each."""
+    9): float in 64-point FFT windows with 65 - ntaps valid outputs each (the
+    reference's tiling), half in 256-point windows (257 - ntaps outputs) on
+    MFMA.  GFLOP/s counts the windows' transforms at 5 N log2 N."""
     import torch
 
     import thunderfft_amd as thff
@@ -275,11 +277,13 @@ def time_conv_valid(T: str, ntaps: int, steps: int, warmup: int) -> dict:
     ms = timed(launch, steps, warmup, stream)
     thff.ThunderFFTFinalize(T)
     nbytes = (length + out_len) * elem
-    windows = -(-out_len // (65 - ntaps))
-    flops = windows * (2 * 5.0 * 64 * 6 + 6.0 * 64)
+    win = 256 if T == "half" else 64
+    windows = -(-out_len // (win + 1 - ntaps))
+    flops = windows * (2 * 5.0 * win * math.log2(win) + 6.0 * win)
     del x, y, taps
-    return {"workload": (f"conv1d_valid {length} x {ntaps} taps {T}2, 64-point windows "
-                         f"({65 - ntaps} outputs each)"),
+    win = 256 if T == "half" else 64  # half: 256-point windows on MFMA; float: 64-point on VALU
+    return {"workload": (f"conv1d_valid {length} x {ntaps} taps {T}2, {win}-point windows "
+                         f"({win + 1 - ntaps} outputs each)"),
             "precision": T, "us_per_call": ms * 1e3, "median_us_per_call": LAST_MEDIAN_MS * 1e3,
             "gflops": flops / (ms * 1e-3) / 1e9,
             "gbps": nbytes / (ms * 1e-3) / 1e9,

@@ -650,3 +650,182 @@ conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict_
 }
 
 }  // namespace thff
+
+namespace thff {
+
+// ---------------------------------------------------------------------------
+// Tiled valid correlation for half2 on MFMA with 256-point windows (the
+// contract of conv1d_valid_kernel, fft_conv.hpp; the reference's
+// conv1d_direct_fft_kernel, sample/conv1d/main.cu:38-128, slides 64-point
+// windows):
+//   y[b][i] = sum_{k < F} x[b][i + k] * f[k],   i < L - F + 1,  1 <= F <= 64.
+// Window w of a signal is x[w V .. w V + 255] with V = 257 - F (193..256
+// valid outputs): its circular convolution with g[m] = f[(256 - m) mod 256]
+// equals y[w V + j] for j < V, which never wrap.  Against 64-point windows
+// this re-reads (F - 1)/256 of the input instead of (F - 1)/64 and moves
+// 4 windows per wave instead of 16, on the two-stage MFMA transform of
+// N = 256 (fft_mfma.hpp, C = 1: a wave owns 4 transforms, one per window).
+// Per wave and group of 4 windows: stage the span x[w0 V .. w0 V + 3 V + 255]
+// in the wave's LDS region (16-byte loads when the signal starts on a
+// 16-byte boundary; zeros past its end), the forward transform straight
+// from the span (window b starts at b V), the product with G = FFT(g) / 256,
+// the inverse as conj(DFT(conj(P))) from registers, then the V valid outputs
+// of each window compacted into the region and stored as one run of 4 V
+// values (16-byte stores when the output signal starts on a 16-byte
+// boundary; w0 V is a multiple of 4 values).
+// Set-up per workgroup, no table but the kernel's own: W_256 twiddles
+// (sincospi, fp32) in LDS, G in fp32 by direct evaluation over the F taps
+// (one bin per lane), the step-2 twiddles and the DFT16 operands.  Nothing
+// crosses waves after the set-up.
+// ---------------------------------------------------------------------------
+template <int N = 256>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void
+conv1d_valid_mfma_kernel(const __half2* __restrict__ x, const float2* __restrict__ taps,
+                         __half2* __restrict__ y, long long len, int ntaps, int batch,
+                         int groups_per_block) {
+    static_assert(N == 256, "256-point windows (the two-stage MFMA transform, C = 1)");
+    using P = MfmaPlan<1>;
+    constexpr int kWindows = P::kBlocks;         // 4 windows per wave
+    constexpr int kGroup = 4 * kWindows;         // windows per workgroup tile
+    static_assert(P::kRegion >= 1024 + 16 * 16, "span of 3 V + 256 <= 1024 values, padded");
+    __shared__ __align__(16) unsigned lds[4 * P::kRegion];
+    __shared__ cpx w1[P::kTw1];
+    __shared__ float2 tw256[N];
+    __shared__ cpx spectrum[N];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int n = lane & 15, q = lane >> 4;
+    unsigned* const region = lds + wave * P::kRegion;
+    const int V = 257 - ntaps;
+
+    {
+        float s, c;
+        sincospif(static_cast<float>(tid) / 128.0f, &s, &c);  // (cos, sin)(2 pi tid / 256)
+        tw256[tid] = make_float2(c, s);
+    }
+    __syncthreads();
+    {
+        // G[k] = (1/256) sum_{k' < F} f[k'] e^(+2 pi i k' k / 256): the forward
+        // transform of g, one bin per lane.
+        const int k = tid;
+        cpx acc{0.f, 0.f};
+        for (int kk = 0; kk < ntaps; ++kk) {
+            const float2 f = taps[kk];
+            const float2 w = tw256[(kk * k) & (N - 1)];
+            acc = cadd(acc, cmul(cpx{f.x, f.y}, cpx{w.x, w.y}));
+        }
+        spectrum[k] = {acc.re * (1.0f / N), acc.im * (1.0f / N)};
+        // step-2 twiddles W_256^(n k1), k1 = q + 4 r (C = 1), forward
+        const int l = tid & 63, r = tid >> 6;
+        const float2 w = tw256[((l & 15) * ((l >> 4) + 4 * r)) & (N - 1)];
+        w1[tid] = cpx{w.x, -w.y};
+    }
+    f16x8 a[2], a_regs[2];
+    dft16_operands<true>(a, lane);
+    dft16_operands<true, true>(a_regs, lane);
+    const Stage3Plain<false> s3{a, nullptr};
+    __syncthreads();
+    // The lane's bins n + 16 (q + 4 r) of G, the same for its 4 windows.
+    cpx gk[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) gk[r] = spectrum[n + 16 * (q + 4 * r)];
+
+    const long long out_len = len - ntaps + 1;
+    const long long windows = (out_len + V - 1) / V;  // per signal
+    const long long groups_per_signal = (windows + kGroup - 1) / kGroup;
+    const long long groups = groups_per_signal * batch;
+    const bool x16 = (reinterpret_cast<unsigned long long>(x) & 15) == 0;
+    const bool y16 = (reinterpret_cast<unsigned long long>(y) & 15) == 0;
+    const int need = 3 * V + N;  // values of the span the wave's windows read
+
+    long long g, g_end, step;
+    tile_walk(groups, groups_per_block, g, g_end, step);
+    for (; g < g_end; g += step) {
+        const long long b = g / groups_per_signal;
+        const long long w0 = (g - b * groups_per_signal) * kGroup + wave * kWindows;
+        const long long span0 = w0 * V;  // a multiple of 4 values
+        if (span0 >= out_len) continue;  // none of the wave's windows has an output
+        const long long avail_l = len - span0 < need ? len - span0 : need;
+        const int avail = static_cast<int>(avail_l);
+        const __half2* src = x + b * len + span0;
+        const bool in_vec = x16 && (b * len) % 4 == 0;
+        const bool out_vec = y16 && (b * out_len) % 4 == 0;
+
+        wave_lds_sync();  // the previous group's reads of the region are done
+        if (in_vec) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = 4 * lane + 256 * i;
+                u32x4 v{};
+                if (e + 4 <= avail) {
+                    v = ld_nt(reinterpret_cast<const u32x4*>(src + e));
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (e + c < avail) v[c] = *reinterpret_cast<const unsigned*>(src + e + c);
+                }
+                *reinterpret_cast<u32x4*>(region + P::in_pad(e)) = v;
+            }
+        } else {
+#pragma unroll 4
+            for (int i = 0; i < 16; ++i) {
+                const int e = lane + 64 * i;
+                region[P::in_pad(e)] = e < avail ? *reinterpret_cast<const unsigned*>(src + e) : 0u;
+            }
+        }
+        wave_lds_sync();
+        // ---- forward: window bb's stage-1 inputs x[bb V + n + 16 j] ----
+        cpx v[kWindows][4];
+#pragma unroll
+        for (int bb = 0; bb < kWindows; ++bb) {
+            const int base = bb * V + n;
+            u32x4 xv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[e] = region[P::in_pad(base + 16 * (4 * q + e))];
+            dft16_block(a, as_f16x8(xv), v[bb]);
+        }
+        mfma_steps2to6<1, true>(region, w1, s3, lane, v);
+        // ---- product with G, inverse = conj(DFT(conj(product))) from registers ----
+#pragma unroll
+        for (int bb = 0; bb < kWindows; ++bb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[bb][r] = cmul(v[bb][r], gk[r]);
+        mfma_stage1_regs<1, true>(a_regs, v);
+        mfma_steps2to6<1, true>(region, w1, s3, lane, v);
+        // ---- the V valid outputs of each window, compacted: window bb, lane (n, q)
+        // holds positions n + 16 (q + 4 r) ----
+        wave_lds_sync();
+#pragma unroll
+        for (int bb = 0; bb < kWindows; ++bb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int p = n + 16 * (q + 4 * r);
+                if (p < V) region[bb * V + p] = pack_half2({v[bb][r].re, -v[bb][r].im});
+            }
+        wave_lds_sync();
+        const long long left = out_len - span0;
+        const int count = left < kWindows * V ? static_cast<int>(left) : kWindows * V;
+        __half2* dst = y + b * out_len + span0;
+        if (out_vec) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = 4 * lane + 256 * i;
+                if (e + 4 <= count) {
+                    st_nt(reinterpret_cast<u32x4*>(dst + e), *reinterpret_cast<const u32x4*>(region + e));
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (e + c < count) *reinterpret_cast<unsigned*>(dst + e + c) = region[e + c];
+                }
+            }
+        } else {
+#pragma unroll 4
+            for (int i = 0; i < 16; ++i) {
+                const int e = lane + 64 * i;
+                if (e < count) *reinterpret_cast<unsigned*>(dst + e) = region[e];
+            }
+        }
+    }
+}
+
+}  // namespace thff

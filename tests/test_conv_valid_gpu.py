@@ -13,8 +13,10 @@ y[i] = sum_k x[i + k] f[k] (:156-174).  Here:
   sample's own comparison against the unrounded fp32 inputs;
 * batches of odd-length signals, input_len == filter_len, every filter
   length 1..64 on a short signal, with output sentinels;
-* at 2^24 samples the exact property that a unit impulse at tap k0 shifts
-  the signal: y[i] = x[i + k0].
+* at 2^24 samples the property that a unit impulse at tap k0 shifts the
+  signal, y[i] = x[i + k0]: per output for float (fp32 arithmetic), against
+  the signal scale for half (its 256-point windows run on MFMA with f16
+  data at each DFT16 stage).
 """
 import numpy as np
 import pytest
@@ -25,6 +27,9 @@ from thff_testlib import GATE, from_device, to_device
 pytestmark = pytest.mark.gpu
 
 TIGHT = {"float": 2e-6, "half": 1e-3}
+# The half path runs its 256-point windows on MFMA with f16 data at each
+# DFT16 stage: per-output errors are bounded against the signal scale.
+HALF_MAX_ABS = 5e-3
 GUARD = 16
 GUARD_VALUE = -271.0 + 137.0j
 
@@ -135,10 +140,17 @@ def test_large_impulse_shifts(T, ntaps, k0):
     y = from_device(d_y, T).reshape(batch, out)
     expect = x[:, k0:k0 + out]
     err = np.abs(y - expect)
-    tol = (1e-6 if T == "float" else 2.0 ** -10) * np.abs(expect) + 1e-6
-    label = f"{T} F={ntaps} k0={k0}: max_err={err.max():.3e}"
+    rel_l2 = float(np.linalg.norm(err) / np.linalg.norm(expect))
+    label = f"{T} F={ntaps} k0={k0}: max_err={err.max():.3e} rel_l2={rel_l2:.3e}"
     print(label, flush=True)
-    assert np.all(np.isfinite(y)) and np.all(err <= tol), label
+    assert np.all(np.isfinite(y)), label
+    if T == "float":
+        # fp32 arithmetic: per-element
+        assert np.all(err <= 1e-6 * np.abs(expect) + 1e-6), label
+    else:
+        # MFMA: f16 data at each DFT16 stage spreads rounding over a window,
+        # so errors are bounded against the signal scale (|x| <= 1)
+        assert err.max() <= HALF_MAX_ABS and rel_l2 <= TIGHT["half"], label
 
 
 @pytest.mark.parametrize("T", ["half", "float"])
@@ -161,12 +173,16 @@ def test_signal_beyond_2e31_values(T):
     d_f = torch.from_numpy(f.view(np.float32)).cuda()
     d_y = torch.full((2 * out,), float("nan"), dtype=dt, device="cuda")
     thff.ThunderFFT_conv1d_valid(T, d_x, length, d_f, ntaps, d_y)
-    tol_rel = 1e-6 if T == "float" else 2.0 ** -10
     for lo, hi in ((0, 1 << 20), ((1 << 31) - (1 << 20), out)):
         y = d_y[2 * lo:2 * hi].float()
         want = d_x[2 * (lo + k0):2 * (hi + k0)].float()
         err = (y - want).abs()
-        ok = bool(torch.isfinite(y).all()) and bool((err <= tol_rel * want.abs() + 1e-6).all())
+        if T == "float":
+            ok = bool((err <= 1e-6 * want.abs() + 1e-6).all())
+        else:  # MFMA: bounded against the signal scale (|x| <= 1)
+            rel_l2 = float(torch.linalg.vector_norm(err) / torch.linalg.vector_norm(want))
+            ok = float(err.max()) <= HALF_MAX_ABS and rel_l2 <= TIGHT["half"]
+        ok = ok and bool(torch.isfinite(y).all())
         print(f"{T} outputs [{lo}, {hi}): max_err={float(err.max()):.3e}", flush=True)
         assert ok, (T, lo, hi)
     del d_x, d_y

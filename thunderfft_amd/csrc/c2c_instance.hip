@@ -334,23 +334,30 @@ hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectr
 hipError_t launch_conv1d_valid(int precision, const void* x, long long len, const float2* taps,
                                int ntaps, void* y, int batch, const float2* tw, int num_cus,
                                hipStream_t stream) {
-    // A group is the 64 windows (one per transform slot) of one workgroup
-    // pass; each workgroup transforms the filter once and walks many groups.
-    // The occupancy in workgroups per CU: fp32 2 (with its span prefetch),
-    // fp16 3.  2^26 values, 9 taps: 232 us fp32 and 162 us fp16, against
-    // 294 / 174 us for runs of 4 groups.
+    // fp32: a group is the 64 windows (one per transform slot) of one
+    // workgroup pass; each workgroup transforms the filter once and walks
+    // many groups, 2 workgroups per CU (the occupancy, with its span
+    // prefetch).  2^26 values, 9 taps: 232 us, against 294 us for runs of 4
+    // groups.
+    // half2: 256-point windows on MFMA (conv1d_valid_mfma_kernel), 16 windows
+    // per workgroup tile, a device grid of 4 workgroups per CU.
+    if (precision != 0) {
+        const long long valid = 257 - ntaps;
+        const long long windows = (len - ntaps + 1 + valid - 1) / valid;
+        const long long groups = (windows + 15) / 16 * batch;
+        const Grid g = make_grid(groups, 4, num_cus);
+        conv1d_valid_mfma_kernel<256><<<g.blocks, 256, 0, stream>>>(
+            static_cast<const __half2*>(x), taps, static_cast<__half2*>(y), len, ntaps, batch,
+            g.tiles_per_block);
+        return hipGetLastError();
+    }
     const long long valid = 65 - ntaps;
     const long long windows = (len - ntaps + 1 + valid - 1) / valid;
     const long long groups = (windows + 63) / 64 * batch;
-    const Grid g = make_grid(groups, precision == 0 ? 2 : 3, num_cus);
-    if (precision == 0)
-        conv1d_valid_kernel<float2><<<g.blocks, 256, 0, stream>>>(
-            static_cast<const float2*>(x), taps, static_cast<float2*>(y), len, ntaps, batch, tw,
-            g.tiles_per_block);
-    else
-        conv1d_valid_kernel<__half2><<<g.blocks, 256, 0, stream>>>(
-            static_cast<const __half2*>(x), taps, static_cast<__half2*>(y), len, ntaps, batch, tw,
-            g.tiles_per_block);
+    const Grid g = make_grid(groups, 2, num_cus);
+    conv1d_valid_kernel<float2><<<g.blocks, 256, 0, stream>>>(
+        static_cast<const float2*>(x), taps, static_cast<float2*>(y), len, ntaps, batch, tw,
+        g.tiles_per_block);
     return hipGetLastError();
 }
 
