@@ -61,6 +61,17 @@ constexpr float kSin16[16] = {
     0.0f, -0.38268343236508977173f, -0.70710678118654752440f, -0.92387953251128675613f,
     -1.0f, -0.92387953251128675613f, -0.70710678118654752440f, -0.38268343236508977173f};
 
+// (cos, sin)(2 pi num / den) for a power-of-two den, computed with the
+// hardware transcendentals (v_cos_f32 / v_sin_f32, whose argument is in
+// revolutions) with no memory access: num is reduced mod den first, so the
+// argument num/den in [0, 1) is exact.  Used where the result is rounded to
+// f16 or applied to data that is (the device API's fp16 coefficients): the
+// table of ThunderFFTInitialize stays the source of every fp32 twiddle.
+__device__ __forceinline__ cpx cis_rev(int num, int den) {
+    const float r = static_cast<float>(num & (den - 1)) / static_cast<float>(den);
+    return {__builtin_amdgcn_cosf(r), __builtin_amdgcn_sinf(r)};
+}
+
 // a * W_R^E with W_R = exp(-2*pi*i/R) (forward) or exp(+2*pi*i/R) (inverse).
 // R divides 16; multiplications by +-1 and +-i cost no multiplies.
 template <int R, int E, bool FWD>

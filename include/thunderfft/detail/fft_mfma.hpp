@@ -340,39 +340,101 @@ __device__ __forceinline__ void mfma_fft_staged(unsigned* region, const f16x8 (&
     mfma_steps2to6<C, FWD>(region, w1, s3, lane, y);
 }
 
+// The DFT16 operands of dft16_operands with the entries computed by cis_rev
+// instead of read from the constant table (no memory access; the f16
+// rounding of each entry dominates the transcendental's error).
+template <bool FWD, bool kInterleaved = false>
+__device__ __forceinline__ void dft16_operands_arith(f16x8 (&a)[2], int lane) {
+    const int m = lane & 15, q = lane >> 4;
+    const int gq = m >> 2, i = m & 3;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int k = gq + 4 * (2 * h + (i >> 1));
+        const int o = i & 1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int kk = 8 * q + e;
+            const int j = kInterleaved ? (kk >> 3) + 4 * ((kk >> 1) & 3) : kk >> 1;
+            const int p = kk & 1;
+            const cpx cs = cis_rev(j * k, 16);
+            const float c = cs.re, s = FWD ? -cs.im : cs.im;
+            const float v = o == 0 ? (p == 0 ? c : -s) : (p == 0 ? s : c);
+            a[h][e] = static_cast<_Float16>(v);
+        }
+    }
+}
+
+// Per-lane coefficients of one direction of the two-stage MFMA transform
+// held in registers (mfma_fft_regs): the stage-1 operands for inputs in the
+// transform's own output layout (a_in, column-permuted), the plain operands,
+// the step-2 twiddles W_N^(t k1) (t = 16c + n, k1 = q + 4r) and the step-4
+// twiddles W_16C^(n m), conjugated for the forward direction.  load() reads
+// the twiddles from the ThunderFFTInitialize table; build() computes
+// everything with cis_rev (the device API's precomputed fp16 coefficients).
+template <int C>
+struct MfmaCoeffs {
+    static constexpr int N = 256 * C;
+    f16x8 a_in[2], a[2];
+    cpx w1[C * 4];
+    cpx w2[C > 1 ? C - 1 : 1];
+
+    template <bool FWD, class Tw>
+    __device__ __forceinline__ void fill(int lane, Tw tw_at) {
+        const int n = lane & 15, q = lane >> 4;
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const cpx x = tw_at((16 * c + n) * (q + 4 * r));
+                w1[c * 4 + r] = FWD ? cpx{x.re, -x.im} : x;
+            }
+#pragma unroll
+        for (int m = 1; m < C; ++m) {
+            const cpx x = tw_at(16 * n * m);
+            w2[m - 1] = FWD ? cpx{x.re, -x.im} : x;
+        }
+    }
+    template <bool FWD>
+    __device__ __forceinline__ void load(const float2* __restrict__ tw, int lane) {
+        dft16_operands<FWD, true>(a_in, lane);
+        dft16_operands<FWD>(a, lane);
+        fill<FWD>(lane, [&](int k) {
+            const float2 x = tw[k & (N - 1)];
+            return cpx{x.x, x.y};
+        });
+    }
+    template <bool FWD>
+    __device__ __forceinline__ void build(int lane) {
+        dft16_operands_arith<FWD, true>(a_in, lane);
+        dft16_operands_arith<FWD>(a, lane);
+        fill<FWD>(lane, [](int k) { return cis_rev(k, N); });
+    }
+};
+
 // One MFMA transform of the kFPW transforms a wave holds in registers, for
 // callers without the workgroup set-up (the device-side API): y[b][r] holds
 // z_f[16 c + n + 16C (q + 4 r)] for block b = (f, c) on entry (the layout the
 // transform leaves, so forward and inverse chain), and
 // X_f[k1 + 16 m + 16C (q + 4 r)] for block b = (f, m), k1 = n, on return.
-// Operands and twiddles are built from the positive-angle table `tw` of
-// length N for this call's direction; `region` is the wave's LDS scratch
-// (16 * kBlocks * 16 dwords), written after a wave-level sync.
+// `k` holds this direction's coefficients; `region` is the wave's LDS
+// scratch (16 * kBlocks * 16 dwords), written after a wave-level sync.
+template <int C, bool FWD>
+__device__ __forceinline__ void mfma_fft_regs(unsigned* region, const MfmaCoeffs<C>& k, int lane,
+                                              cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
+    mfma_stage1_regs<C>(k.a_in, y);
+    mfma_steps2to6_w<C, FWD>(
+        region, [&](int c, int r) { return k.w1[c * 4 + r]; }, Stage3Plain<false>{k.a, k.w2}, lane,
+        y);
+}
+
+// As above, the coefficients read from the positive-angle table `tw` of
+// length N for this call.
 template <int C, bool FWD>
 __device__ __forceinline__ void mfma_fft_regs(unsigned* region, const float2* __restrict__ tw,
                                               int lane, cpx (&y)[MfmaPlan<C>::kBlocks][4]) {
-    constexpr int N = MfmaPlan<C>::N;
-    const int n = lane & 15, q = lane >> 4;
-    f16x8 a_in[2], a[2];
-    dft16_operands<FWD, true>(a_in, lane);
-    dft16_operands<FWD>(a, lane);
-    cpx w1[C * 4];
-#pragma unroll
-    for (int c = 0; c < C; ++c)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float2 x = tw[((16 * c + n) * (q + 4 * r)) & (N - 1)];
-            w1[c * 4 + r] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
-        }
-    cpx w2[C > 1 ? C - 1 : 1];
-#pragma unroll
-    for (int m = 1; m < C; ++m) {
-        const float2 x = tw[(16 * n * m) & (N - 1)];
-        w2[m - 1] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
-    }
-    mfma_stage1_regs<C>(a_in, y);
-    mfma_steps2to6_w<C, FWD>(
-        region, [&](int c, int r) { return w1[c * 4 + r]; }, Stage3Plain<false>{a, w2}, lane, y);
+    MfmaCoeffs<C> k;
+    k.template load<FWD>(tw, lane);
+    mfma_fft_regs<C, FWD>(region, k, lane, y);
 }
 
 // Batched C2C of half2 signals of N = 256*C on MFMA (C = 4 is N = 1024 as
@@ -516,6 +578,49 @@ __device__ __forceinline__ int xaddr4096(int k1, int t0, int t1) {
     return Mfma4096::kMatrix * k1 + 16 * t0 + 4 * (((t1 >> 2) + (t0 >> 2)) & 3) + ((t1 + k1) & 3);
 }
 
+// Per-lane coefficients of one direction of mfma4096_fft_regs: plain and
+// column-permuted DFT16 operands, the stage-1 -> 2 twiddles
+// W^((4 w + b + 16 n)(q + 4 r)) and the stage-2 -> 3 twiddles W^(16 n (q + 4 r)),
+// conjugated for the forward direction (tid: the lane's index in the
+// 256-lane block).  load() from the table, build() with cis_rev.
+struct Mfma4096Coeffs {
+    static constexpr int N = 4096;
+    f16x8 a[2], a_in[2];
+    cpx w1[4][4], w2[4];
+
+    template <bool FWD, class Tw>
+    __device__ __forceinline__ void fill(int tid, Tw tw_at) {
+        const int wave = tid >> 6, lane = tid & 63, n = lane & 15, q = lane >> 4;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const cpx x = tw_at((4 * wave + b + 16 * n) * (q + 4 * r));
+                w1[b][r] = FWD ? cpx{x.re, -x.im} : x;
+            }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const cpx x = tw_at(16 * n * (q + 4 * r));
+            w2[r] = FWD ? cpx{x.re, -x.im} : x;
+        }
+    }
+    template <bool FWD>
+    __device__ __forceinline__ void load(const float2* __restrict__ tw, int tid) {
+        dft16_operands<FWD>(a, tid & 63);
+        dft16_operands<FWD, true>(a_in, tid & 63);
+        fill<FWD>(tid, [&](int k) {
+            const float2 x = tw[k & (N - 1)];
+            return cpx{x.x, x.y};
+        });
+    }
+    template <bool FWD>
+    __device__ __forceinline__ void build(int tid) {
+        dft16_operands_arith<FWD>(a, tid & 63);
+        dft16_operands_arith<FWD, true>(a_in, tid & 63);
+        fill<FWD>(tid, [](int k) { return cis_rev(k, N); });
+    }
+};
+
 // One N = 4096 transform per workgroup from registers, either direction, for
 // callers without the kernel's set-up (the device-side API).  Lane (n, q) of
 // wave w holds, in v[b][r], element 4 w + b + 16 n + 256 (q + 4 r) on entry
@@ -524,30 +629,22 @@ __device__ __forceinline__ int xaddr4096(int k1, int t0, int t1) {
 // (column-permuted operands), W^(t' k1), the workgroup exchange with
 // t0 = 4 w + b, t1 = n, stage 2, W_256^(t0 k2), the wave-local transpose
 // and stage 3.  xbuf: Mfma4096::kExchange dwords of LDS; two workgroup
-// barriers, the first before xbuf is written.  Operands and twiddles come
-// from the positive-angle table `tw` of length 4096.
+// barriers, the first before xbuf is written.  `k` holds this direction's
+// coefficients.
 template <bool FWD>
-__device__ __forceinline__ void mfma4096_fft_regs(unsigned* xbuf, const float2* __restrict__ tw,
-                                                  int tid, cpx (&v)[4][4]) {
+__device__ __forceinline__ void mfma4096_fft_regs(unsigned* xbuf, const Mfma4096Coeffs& k, int tid,
+                                                  cpx (&v)[4][4]) {
     using P = Mfma4096;
-    constexpr int N = P::N;
     const int wave = tid >> 6, lane = tid & 63, n = lane & 15, q = lane >> 4;
     unsigned* const region = xbuf + 4 * P::kMatrix * wave;
-    f16x8 a[2], a_in[2];
-    dft16_operands<FWD>(a, lane);
-    dft16_operands<FWD, true>(a_in, lane);
-    auto tw_at = [&](int k) {
-        const float2 x = tw[k & (N - 1)];
-        return FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
-    };
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
         u32x4 xv;
 #pragma unroll
         for (int r = 0; r < 4; ++r) xv[r] = pack_half2(v[b][r]);
-        dft16_block(a_in, as_f16x8(xv), v[b]);
+        dft16_block(k.a_in, as_f16x8(xv), v[b]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], tw_at((4 * wave + b + 16 * n) * (q + 4 * r)));
+        for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], k.w1[b][r]);
     }
     __syncthreads();  // every wave is done with xbuf
 #pragma unroll
@@ -562,9 +659,9 @@ __device__ __forceinline__ void mfma4096_fft_regs(unsigned* xbuf, const float2* 
         u32x4 xv;  // t1 = 4 q + e sits at position (e + k1) & 3 = (e + b) & 3
 #pragma unroll
         for (int e = 0; e < 4; ++e) xv[e] = raw[(e + b) & 3];
-        dft16_block(a, as_f16x8(xv), v[b]);
+        dft16_block(k.a, as_f16x8(xv), v[b]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], tw_at(16 * n * (q + 4 * r)));
+        for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], k.w2[r]);
     }
     wave_lds_sync();
 #pragma unroll
@@ -577,8 +674,18 @@ __device__ __forceinline__ void mfma4096_fft_regs(unsigned* xbuf, const float2* 
     for (int b = 0; b < 4; ++b) {
         const u32x4 xv = *reinterpret_cast<const u32x4*>(
             region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
-        dft16_block(a, as_f16x8(xv), v[b]);
+        dft16_block(k.a, as_f16x8(xv), v[b]);
     }
+}
+
+// As above, the coefficients read from the positive-angle table `tw` of
+// length 4096 for this call.
+template <bool FWD>
+__device__ __forceinline__ void mfma4096_fft_regs(unsigned* xbuf, const float2* __restrict__ tw,
+                                                  int tid, cpx (&v)[4][4]) {
+    Mfma4096Coeffs k;
+    k.template load<FWD>(tw, tid);
+    mfma4096_fft_regs<FWD>(xbuf, k, tid, v);
 }
 
 template <bool FWD, bool kPrefetch>

@@ -92,6 +92,19 @@ struct PassTwiddles {
         }
     }
 
+    // The same factors from cis_rev, with no table access.
+    __device__ __forceinline__ void build(int t) {
+        const int k = t % L;
+        auto w = [&](int j) { return cis_rev(j * k * (N / (L * R)), N); };
+        if constexpr (kCompact) {
+            b[0] = w(1), b[1] = w(2), b[2] = w(3);
+            b[3] = w(4), b[4] = w(8), b[5] = w(12);
+        } else {
+#pragma unroll
+            for (int j = 1; j < R; ++j) b[j - 1] = w(j);
+        }
+    }
+
     // All R-1 bases W_{LR}^{j*(t mod L)}, j = 1..R-1.
     __device__ __forceinline__ void expand(cpx* w) const {
         if constexpr (kCompact) {
@@ -120,6 +133,13 @@ struct LaneTwiddles {
         table = tw;
         p1.load(t, tw);
         if constexpr (P::kR2 > 1) p2.load(t, tw);
+    }
+    // The factors from cis_rev, with no table (the device API's fp16
+    // coefficients, unit_fp16::make_reg_b_precompute).
+    __device__ __forceinline__ void build(int t) {
+        table = nullptr;
+        p1.build(t);
+        if constexpr (P::kR2 > 1) p2.build(t);
     }
 };
 

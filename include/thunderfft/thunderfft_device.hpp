@@ -34,7 +34,12 @@
 //  * Twiddles: ThunderFFTInitialize<T>(N) builds the device table; pass its
 //    pointer (ThunderFFT_twiddle_table<T>() on the host) to
 //    ThunderFFT_load_twiddles once per kernel, or straight to
-//    ThunderFFT_kernel_reg, which then loads the lane's factors itself.
+//    ThunderFFT_kernel_reg, which then loads the lane's factors itself.  For
+//    half, as in the reference's fused samples, a kernel can instead build
+//    its coefficients once with unit_fp16::make_reg_b_precompute<N, fwd>(W)
+//    (vec2_t<half> W[unit_fp16::coefficient_count<N>]; no table needed) and
+//    pass W to ThunderFFT_kernel_reg: the MFMA transforms then build no
+//    operand and read no twiddle per call.
 //  * layout_t::Reversed must be false: fragments here are natural-order.
 #pragma once
 
@@ -231,6 +236,97 @@ __device__ __forceinline__ void ThunderFFT_kernel_reg(vec2_t<T>* __restrict__ re
     ThunderFFT_kernel_reg<T, N, batch, forward>(reg, w, workspace);
 }
 
+namespace detail {
+
+// The per-lane coefficients of the fp16 transform of length N: the MFMA
+// transforms' operands and twiddles (N = 256, 512, 1024, 4096) or the VALU
+// passes' twiddle factors (N = 64, 128, 2048).
+template <int N>
+using half_coefficients = std::conditional_t<
+    N == 4096, thff::Mfma4096Coeffs,
+    std::conditional_t<fragment_on_mfma<half, N>, thff::MfmaCoeffs<(N >= 256 ? N / 256 : 1)>,
+                       thff::LaneTwiddles<N>>>;
+
+}  // namespace detail
+
+namespace unit_fp16 {
+
+// half2 slots of per-lane coefficients that make_reg_b_precompute<N, fwd>
+// writes and ThunderFFT_kernel_reg<half, N, batch, fwd>(reg, W, workspace)
+// reads (a slot holds 32 bits: f16 operand pairs or one fp32 twiddle
+// component).  The reference's arrays are 28 or 36 half2 (unit_kernel_fp16.cuh
+// :97-108); declare W[coefficient_count<N>] instead.
+template <int N>
+inline constexpr int coefficient_count =
+    static_cast<int>(sizeof(detail::half_coefficients<N>) / sizeof(unsigned));
+
+// This lane's coefficients of the fp16 transform of length N in direction
+// `forward` (the reference's unit_fp16::make_reg_b_precompute<N, fwd>,
+// unit_kernel_fp16.cuh:97-108, and sample/README.md:406-409): the DFT16
+// operands and every twiddle the transform needs, computed with the hardware
+// transcendentals (no table, no memory access; their error is far below the
+// f16 rounding of the data), once per kernel.  Call with the same block
+// shape and lane numbering as ThunderFFT_kernel_reg.
+template <int N, bool forward>
+__device__ __forceinline__ void make_reg_b_precompute(vec2_t<half>* W) {
+    detail::check_shape<N, batch_per_block<N>>();
+    const int tid = detail::block_tid();
+    detail::half_coefficients<N> k;
+    if constexpr (N == 4096)
+        k.template build<forward>(tid);
+    else if constexpr (fragment_on_mfma<half, N>)
+        k.template build<forward>(tid & 63);
+    else
+        k.build(tid % (N / 16));
+    __builtin_memcpy(static_cast<void*>(W), &k, sizeof(k));
+}
+
+}  // namespace unit_fp16
+
+// ThunderFFT_kernel_reg with the reference's argument types
+// (thunderfft.cuh:200-202): for half, W holds this lane's coefficients from
+// unit_fp16::make_reg_b_precompute<N, forward> (unit_fp16::coefficient_count<N>
+// slots), so no table is read and no operand is built per call; for float, W
+// is the ThunderFFTInitialize<float>(N) table, as in the overload above.
+template <typename T, int N, int batch, bool forward>
+__device__ __forceinline__ void ThunderFFT_kernel_reg(vec2_t<T>* __restrict__ reg,
+                                                      vec2_t<T>* __restrict__ W, void* workspace) {
+    if constexpr (std::is_same_v<T, float>) {
+        ThunderFFT_kernel_reg<T, N, batch, forward>(reg, static_cast<const float2*>(W), workspace);
+    } else {
+        detail::check_shape<N, batch>();
+        const int tid = detail::block_tid();
+        detail::half_coefficients<N> k;
+        __builtin_memcpy(&k, static_cast<const void*>(W), sizeof(k));
+        if constexpr (N == 4096) {
+            thff::cpx y[4][4];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) y[j >> 2][j & 3] = detail::to_cpx<T>(reg[j]);
+            thff::mfma4096_fft_regs<forward>(static_cast<unsigned*>(workspace), k, tid, y);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) reg[j] = detail::from_cpx<T>(y[j >> 2][j & 3]);
+        } else if constexpr (fragment_on_mfma<T, N>) {
+            constexpr int C = N / 256;
+            thff::cpx y[4][4];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) y[j >> 2][j & 3] = detail::to_cpx<T>(reg[j]);
+            unsigned* region = static_cast<unsigned*>(workspace) + (tid >> 6) * 1024;
+            thff::mfma_fft_regs<C, forward>(region, k, tid & 63, y);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) reg[j] = detail::from_cpx<T>(y[j >> 2][j & 3]);
+        } else {
+            using P = thff::C2CPlan<N>;
+            thff::cpx* slot = static_cast<thff::cpx*>(workspace) + (tid / P::kTPF) * P::kSlot;
+            thff::cpx v[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = detail::to_cpx<T>(reg[j]);
+            thff::fft_registers<N, forward>(v, slot, tid % P::kTPF, k);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) reg[j] = detail::from_cpx<T>(v[j]);
+        }
+    }
+}
+
 // Global memory -> fragment (reference thunderfft.cuh:81-85).  gmem is the
 // block-local base of `batch` contiguous natural-order signals of N values.
 template <typename T, int N, int batch>
@@ -284,8 +380,23 @@ template <typename T, typename sL>
 __device__ __forceinline__ void ThunderFFT_gmem2smem(vec2_t<T>* __restrict__ smem,
                                                      const vec2_t<T>* __restrict__ gmem) {
     const int tid = detail::block_tid();
+    constexpr int kTotal = sL::N * sL::batch;
+    constexpr int kVec = 16 / static_cast<int>(sizeof(vec2_t<T>));  // values per 16-byte load
+    constexpr bool kWhole = kTotal % (256 * kVec) == 0;
+    if (kWhole && (reinterpret_cast<unsigned long long>(gmem) & 15) == 0) {
+        // 16-byte loads of kVec consecutive values
 #pragma unroll 4
-    for (int e = tid; e < sL::N * sL::batch; e += 256) smem[sL::at(e % sL::N, e / sL::N)] = gmem[e];
+        for (int e = kVec * tid; e < kTotal; e += 256 * kVec) {
+            const thff::u32x4 w = thff::ld_nt(reinterpret_cast<const thff::u32x4*>(gmem + e));
+            vec2_t<T> v[kVec];
+            __builtin_memcpy(v, &w, 16);
+#pragma unroll
+            for (int c = 0; c < kVec; ++c) smem[sL::at((e + c) % sL::N, (e + c) / sL::N)] = v[c];
+        }
+    } else {
+#pragma unroll 4
+        for (int e = tid; e < kTotal; e += 256) smem[sL::at(e % sL::N, e / sL::N)] = gmem[e];
+    }
 }
 
 // Shared memory described by sL -> contiguous global tile (reference
@@ -294,8 +405,23 @@ template <typename T, typename sL>
 __device__ __forceinline__ void ThunderFFT_smem2gmem(vec2_t<T>* __restrict__ gmem,
                                                      const vec2_t<T>* __restrict__ smem) {
     const int tid = detail::block_tid();
+    constexpr int kTotal = sL::N * sL::batch;
+    constexpr int kVec = 16 / static_cast<int>(sizeof(vec2_t<T>));
+    constexpr bool kWhole = kTotal % (256 * kVec) == 0;
+    if (kWhole && (reinterpret_cast<unsigned long long>(gmem) & 15) == 0) {
 #pragma unroll 4
-    for (int e = tid; e < sL::N * sL::batch; e += 256) gmem[e] = smem[sL::at(e % sL::N, e / sL::N)];
+        for (int e = kVec * tid; e < kTotal; e += 256 * kVec) {
+            vec2_t<T> v[kVec];
+#pragma unroll
+            for (int c = 0; c < kVec; ++c) v[c] = smem[sL::at((e + c) % sL::N, (e + c) / sL::N)];
+            thff::u32x4 w;
+            __builtin_memcpy(&w, v, 16);
+            thff::st_nt(reinterpret_cast<thff::u32x4*>(gmem + e), w);
+        }
+    } else {
+#pragma unroll 4
+        for (int e = tid; e < kTotal; e += 256) gmem[e] = smem[sL::at(e % sL::N, e / sL::N)];
+    }
 }
 
 }  // namespace thunderfft

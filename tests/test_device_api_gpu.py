@@ -9,7 +9,11 @@ thunderfft_amd/_build/libthff_device_example.so) are run through ctypes:
   ThunderFFT_kernel_reg -> smem -> gmem, with 64 workspace sentinels that must
   survive;
 * the same through ThunderFFT_gmem2reg / reg2gmem only;
-* a fused forward FFT x per-bin filter x inverse FFT / N.
+* a fused forward FFT x per-bin filter x inverse FFT / N;
+* both again through ThunderFFT_kernel_reg(reg, W, workspace) in the
+  reference's argument types, W for half from
+  unit_fp16::make_reg_b_precompute<N, fwd> (the reference's fused-sample
+  pattern, sample/README.md:406-409), for float the table.
 
 Every length x {float, half} x {forward, inverse} against the fp64 oracle;
 the float results must also agree with ThunderFFT_global's to rel L2 1e-6
@@ -48,6 +52,8 @@ def ex():
     L.thffx_device_fft_reg.argtypes = [ci, ci, ci, vp, vp, ci, vp]
     L.thffx_fused_filter.argtypes = [ci, ci, vp, vp, vp, ci, vp]
     L.thffx_fragment_map.argtypes = [ci, ci, vp, vp]
+    L.thffx_device_fft_w.argtypes = [ci, ci, ci, vp, vp, ci, vp]
+    L.thffx_fused_filter_w.argtypes = [ci, ci, vp, vp, vp, ci, vp]
     yield L
     thff.ThunderFFTFinalize("float")
     thff.ThunderFFTFinalize("half")
@@ -116,6 +122,40 @@ def test_device_api_fused_filter(ex, T, n):
     # half: the spectrum is also rounded to binary16 between the transforms
     assert m["nonfinite"] == 0 and m["rel_l2"] <= GATE
     assert m["rel_l2"] <= (5e-6 if T == "float" else 2e-3), label
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("n", SIZES)
+def test_device_api_precomputed_coefficients(ex, T, n):
+    """ThunderFFT_kernel_reg(reg, W, ws): half with per-lane coefficients
+    built by make_reg_b_precompute (no table), float with the table; every
+    length and direction against the oracle, and the fused filter."""
+    import thunderfft_amd as thff
+
+    bpb = thff.transforms_per_block(n)
+    batch = 2 * bpb
+    thff.ThunderFFTInitialize(T, n)
+    x = oracle.represent(oracle.uniform(n, batch, seed=53 + n), T)
+    d_x = to_device(x, T)
+    for forward in (True, False):
+        d_y = to_device(np.full((batch, n), np.nan, dtype=np.complex64), T)
+        assert ex.thffx_device_fft_w(PREC[T], n, int(forward), d_x.data_ptr(), d_y.data_ptr(),
+                                     batch, None) == 0
+        m = oracle.metrics(from_device(d_y, T).reshape(batch, n), oracle.fft(x, forward))
+        label = f"device API (W) {T} N={n} {'fwd' if forward else 'inv'}: rel_l2={m['rel_l2']:.3e}"
+        print(label, flush=True)
+        assert m["nonfinite"] == 0 and m["rel_l2"] <= GATE and m["rel_l2"] <= TIGHT[T], label
+    rng = np.random.default_rng(n + 1)
+    H = (rng.normal(size=n) + 1j * rng.normal(size=n)).astype(np.complex64)
+    d_h = to_device(H, "float")
+    d_y = to_device(np.full((batch, n), np.nan, dtype=np.complex64), T)
+    assert ex.thffx_fused_filter_w(PREC[T], n, d_x.data_ptr(), d_y.data_ptr(), d_h.data_ptr(),
+                                   batch, None) == 0
+    ref = oracle.fft(oracle.fft(x, True) * H.astype(np.complex128)[None, :], False) / n
+    m = oracle.metrics(from_device(d_y, T).reshape(batch, n), ref)
+    label = f"device API fused filter (W) {T} N={n}: rel_l2={m['rel_l2']:.3e}"
+    print(label, flush=True)
+    assert m["nonfinite"] == 0 and m["rel_l2"] <= (5e-6 if T == "float" else 2e-3), label
 
 
 @pytest.mark.parametrize("T", ["float", "half"])

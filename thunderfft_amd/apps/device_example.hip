@@ -8,10 +8,17 @@
 //                         validate_core, sample/validation/fft_validation.cu:84-123);
 //   thffx_device_fft_reg  the same through ThunderFFT_gmem2reg / reg2gmem only;
 //   thffx_fused_filter    forward FFT x per-bin filter x inverse FFT / N in one
-//                         kernel (the reference's fused-convolution pattern).
+//                         kernel (the reference's fused-convolution pattern);
+//   thffx_device_fft_w, thffx_fused_filter_w
+//                         the same two with ThunderFFT_kernel_reg(reg, W, ws) in
+//                         the reference's argument types: for half, W from
+//                         unit_fp16::make_reg_b_precompute<N, fwd> (built once
+//                         per kernel, no table), for float the table.
 // Every entry point requires batch to be a multiple of batch_per_block<N>
 // and returns 0, -22 (bad argument) or -5 (launch error).
 #include <thunderfft/thunderfft.cuh>
+
+#include <type_traits>
 
 namespace {
 
@@ -94,6 +101,65 @@ __global__ __launch_bounds__(256) void fused_filter(const vec2_t<T>* in, vec2_t<
     thunderfft::ThunderFFT_reg2gmem<T, N, BPB>(out + blockIdx.x * BPB * N, reg);
 }
 
+// The coefficient argument of ThunderFFT_kernel_reg(reg, W, ws) in the
+// reference's types: half -> this lane's precomputed coefficients, float ->
+// the table.
+template <class T, int N, bool FWD>
+struct KernelRegW {
+    vec2_t<T> coeffs[std::is_same_v<T, half> ? thunderfft::unit_fp16::coefficient_count<N> : 1];
+    vec2_t<T>* w;
+    __device__ explicit KernelRegW(const float2* tw) {
+        if constexpr (std::is_same_v<T, half>) {
+            thunderfft::unit_fp16::make_reg_b_precompute<N, FWD>(coeffs);
+            w = coeffs;
+        } else {
+            w = const_cast<float2*>(tw);
+        }
+    }
+};
+
+template <class T, int N, bool FWD>
+__global__ __launch_bounds__(256) void device_fft_w(const vec2_t<T>* in, vec2_t<T>* out,
+                                                    const float2* tw) {
+    constexpr int BPB = thunderfft::batch_per_block<N>;
+    __shared__ __align__(16) unsigned char work[thunderfft::workspace_bytes<N, BPB>];
+    KernelRegW<T, N, FWD> W(tw);
+    vec2_t<T> reg[thunderfft::elements_per_thread];
+    thunderfft::ThunderFFT_gmem2reg<T, N, BPB>(reg, in + blockIdx.x * BPB * N);
+    thunderfft::ThunderFFT_kernel_reg<T, N, BPB, FWD>(reg, W.w, work);
+    thunderfft::ThunderFFT_reg2gmem<T, N, BPB>(out + blockIdx.x * BPB * N, reg);
+}
+
+// fused_filter with precomputed coefficients of both directions.
+template <class T, int N>
+__global__ __launch_bounds__(256) void fused_filter_w(const vec2_t<T>* in, vec2_t<T>* out,
+                                                      const float2* H, const float2* tw) {
+    constexpr int BPB = thunderfft::batch_per_block<N>;
+    __shared__ __align__(16) unsigned char work[thunderfft::workspace_bytes<N, BPB>];
+    KernelRegW<T, N, true> Wf(tw);
+    KernelRegW<T, N, false> Wi(tw);
+    vec2_t<T> reg[thunderfft::elements_per_thread];
+    thunderfft::ThunderFFT_gmem2reg<T, N, BPB>(reg, in + blockIdx.x * BPB * N);
+    thunderfft::ThunderFFT_kernel_reg<T, N, BPB, true>(reg, Wf.w, work);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        float2 a;
+        if constexpr (sizeof(vec2_t<T>) == 8)
+            a = reinterpret_cast<const float2&>(reg[j]);
+        else
+            a = __half22float2(reinterpret_cast<const __half2&>(reg[j]));
+        const float2 h = H[thunderfft::fragment_element<T, N>(threadIdx.x, j)];
+        const float2 p = make_float2((a.x * h.x - a.y * h.y) / N, (a.x * h.y + a.y * h.x) / N);
+        if constexpr (sizeof(vec2_t<T>) == 8)
+            reinterpret_cast<float2&>(reg[j]) = p;
+        else
+            reinterpret_cast<__half2&>(reg[j]) = __floats2half2_rn(p.x, p.y);
+    }
+    __syncthreads();  // the forward transform's workspace reads are done
+    thunderfft::ThunderFFT_kernel_reg<T, N, BPB, false>(reg, Wi.w, work);
+    thunderfft::ThunderFFT_reg2gmem<T, N, BPB>(out + blockIdx.x * BPB * N, reg);
+}
+
 // (transform, element) of every (lane, register) of one block:
 // map[2 * (16 * tid + j)] = fragment_transform, [... + 1] = fragment_element.
 template <class T, int N>
@@ -135,8 +201,13 @@ int launch(int kind, int forward, const void* x, void* y, const void* H, int bat
     } else if (kind == 1) {
         if (forward) device_fft_reg<T, N, true><<<grid, 256, 0, s>>>(in, out, tw);
         else device_fft_reg<T, N, false><<<grid, 256, 0, s>>>(in, out, tw);
-    } else {
+    } else if (kind == 2) {
         fused_filter<T, N><<<grid, 256, 0, s>>>(in, out, static_cast<const float2*>(H), tw);
+    } else if (kind == 3) {
+        if (forward) device_fft_w<T, N, true><<<grid, 256, 0, s>>>(in, out, tw);
+        else device_fft_w<T, N, false><<<grid, 256, 0, s>>>(in, out, tw);
+    } else {
+        fused_filter_w<T, N><<<grid, 256, 0, s>>>(in, out, static_cast<const float2*>(H), tw);
     }
     return hipGetLastError() == hipSuccess && hipStreamSynchronize(s) == hipSuccess ? 0 : -5;
 }
@@ -158,7 +229,7 @@ int dispatch(int n, int kind, int forward, const void* x, void* y, const void* H
 
 int run(int precision, int n, int kind, int forward, const void* x, void* y, const void* H,
         int batch, int* guard, void* stream) {
-    if (!x || !y || x == y || (kind == 0 && !guard) || (kind == 2 && !H)) return -22;
+    if (!x || !y || x == y || (kind == 0 && !guard) || ((kind == 2 || kind == 4) && !H)) return -22;
     const void* table = nullptr;
     int tn = 0;
     if (thff_twiddle_info(precision, &table, &tn) != 0 || tn != n || !table) return -22;
@@ -189,5 +260,13 @@ int thffx_device_fft_reg(int precision, int n, int forward, const void* x, void*
 int thffx_fused_filter(int precision, int n, const void* x, void* y, const void* d_filter,
                        int batch, void* stream) {
     return run(precision, n, 2, 1, x, y, d_filter, batch, nullptr, stream);
+}
+int thffx_device_fft_w(int precision, int n, int forward, const void* x, void* y, int batch,
+                       void* stream) {
+    return run(precision, n, 3, forward, x, y, nullptr, batch, nullptr, stream);
+}
+int thffx_fused_filter_w(int precision, int n, const void* x, void* y, const void* d_filter,
+                         int batch, void* stream) {
+    return run(precision, n, 4, 1, x, y, d_filter, batch, nullptr, stream);
 }
 }

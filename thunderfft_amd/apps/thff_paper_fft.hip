@@ -23,6 +23,8 @@
 #include <hipfft/hipfft.h>
 #include <thunderfft/thunderfft.cuh>
 
+#include <type_traits>
+
 #include <cmath>
 #include <cstdio>
 #include <stdexcept>
@@ -92,8 +94,23 @@ __global__ __launch_bounds__(256) void repeat_kernel(const vec2_t<T>* __restrict
     using L = thunderfft::fragment_layout<T, N>;
     __shared__ __align__(16) unsigned char work[thunderfft::workspace_bytes<N, BPB>];
     auto* staged = reinterpret_cast<vec2_t<T>*>(work);
-    thunderfft::lane_twiddles<N> w;
-    thunderfft::ThunderFFT_load_twiddles<N>(w, table);
+    // float: the lane's twiddle factors from the table; half: the per-lane
+    // coefficients of unit_fp16::make_reg_b_precompute, built once here as
+    // in the reference's fused samples (sample/README.md:406-409).
+    thunderfft::lane_twiddles<N> tw_lane;
+    vec2_t<T> coeffs[std::is_same_v<T, half> ? thunderfft::unit_fp16::coefficient_count<N> : 1];
+    if constexpr (std::is_same_v<T, half>)
+        thunderfft::unit_fp16::make_reg_b_precompute<N, true>(coeffs);
+    else
+        thunderfft::ThunderFFT_load_twiddles<N>(tw_lane, table);
+    auto fft = [&](vec2_t<T>* reg) {
+        if constexpr (std::is_same_v<T, half>)
+            thunderfft::ThunderFFT_kernel_reg<T, N, thunderfft::batch_per_block<N>, true>(reg, coeffs,
+                                                                                      work);
+        else
+            thunderfft::ThunderFFT_kernel_reg<T, N, thunderfft::batch_per_block<N>, true>(reg, tw_lane,
+                                                                                      work);
+    };
     vec2_t<T> reg[thunderfft::elements_per_thread];
 
     thunderfft::ThunderFFT_gmem2smem<T, L>(staged, in + static_cast<size_t>(blockIdx.x) * BPB * N);
@@ -102,7 +119,7 @@ __global__ __launch_bounds__(256) void repeat_kernel(const vec2_t<T>* __restrict
         for (unsigned r = 0; r < repeats; ++r) {
             thunderfft::ThunderFFT_smem2reg<T, L>(reg, staged);
             __syncthreads();
-            thunderfft::ThunderFFT_kernel_reg<T, N, BPB, true>(reg, w, work);
+            fft(reg);
             __syncthreads();
             thunderfft::ThunderFFT_reg2smem<T, L>(staged, reg);
             __syncthreads();
@@ -111,7 +128,7 @@ __global__ __launch_bounds__(256) void repeat_kernel(const vec2_t<T>* __restrict
         thunderfft::ThunderFFT_smem2reg<T, L>(reg, staged);
         __syncthreads();
         for (unsigned r = 0; r < repeats; ++r) {
-            thunderfft::ThunderFFT_kernel_reg<T, N, BPB, true>(reg, w, work);
+            fft(reg);
             __syncthreads();
         }
         thunderfft::ThunderFFT_reg2smem<T, L>(staged, reg);
