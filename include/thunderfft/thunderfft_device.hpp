@@ -40,7 +40,8 @@
 //    (vec2_t<half> W[unit_fp16::coefficient_count<N>]; no table needed) and
 //    pass W to ThunderFFT_kernel_reg: the MFMA transforms then build no
 //    operand and read no twiddle per call.
-//  * layout_t::Reversed must be false: fragments here are natural-order.
+//  * layout_t::Reversed on an input layout selects the permutation the
+//    transforms expect, which here is the identity (natural order).
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -70,7 +71,15 @@ inline constexpr int workspace_bytes = 8 * (N + N / 16) * batch;
 
 // Block-local shared-memory layout (reference thunderfft.cuh:35-44): logical
 // element i of transform j is at idx = i*ElemStride + j*BatchStride, stored
-// at idx + (idx / PadPeriod) * Pad.
+// at idx + (idx / PadPeriod) * Pad.  Reversed requests "the input
+// permutation each size-specific transform expects" (the reference's
+// documented meaning, thunderfft.cuh:29-32; its transforms take base-4
+// digit-reversed input for N outside {512, 2048, 4096}).  Every transform
+// here takes natural order, so that permutation is the identity: a fused
+// kernel written for the reference with a reversed input layout runs
+// unchanged.  As in the reference (thunderfft_impl_helper.cuh:51-56), an
+// output layout must not be reversed: ThunderFFT_smem2gmem rejects it at
+// compile time.
 template <int N_, int Batch_, int ElemStride_, int BatchStride_, int PadPeriod_, int Pad_,
           bool Reversed_>
 struct layout_t {
@@ -82,7 +91,6 @@ struct layout_t {
     static constexpr int pad = Pad_;
     static constexpr int reversed = Reversed_;
     static_assert(PadPeriod_ > 0, "layout_t: PadPeriod must be positive");
-    static_assert(!Reversed_, "layout_t: fragments are natural-order; Reversed is not used");
     __host__ __device__ static constexpr int at(int i, int j) {
         const int idx = i * ElemStride_ + j * BatchStride_;
         return idx + (idx / PadPeriod_) * Pad_;
@@ -404,6 +412,7 @@ __device__ __forceinline__ void ThunderFFT_gmem2smem(vec2_t<T>* __restrict__ sme
 template <typename T, typename sL>
 __device__ __forceinline__ void ThunderFFT_smem2gmem(vec2_t<T>* __restrict__ gmem,
                                                      const vec2_t<T>* __restrict__ smem) {
+    static_assert(!sL::reversed, "ThunderFFT_smem2gmem: an output layout must not be reversed");
     const int tid = detail::block_tid();
     constexpr int kTotal = sL::N * sL::batch;
     constexpr int kVec = 16 / static_cast<int>(sizeof(vec2_t<T>));

@@ -53,6 +53,7 @@ def ex():
     L.thffx_fused_filter.argtypes = [ci, ci, vp, vp, vp, ci, vp]
     L.thffx_fragment_map.argtypes = [ci, ci, vp, vp]
     L.thffx_device_fft_w.argtypes = [ci, ci, ci, vp, vp, ci, vp]
+    L.thffx_device_fft_reversed_in.argtypes = [ci, ci, ci, vp, vp, ci, vp, vp]
     L.thffx_fused_filter_w.argtypes = [ci, ci, vp, vp, vp, ci, vp]
     yield L
     thff.ThunderFFTFinalize("float")
@@ -76,11 +77,15 @@ def test_device_api_fft(ex, T, n):
         ref = oracle.fft(x, forward)
         d_lib = torch.empty_like(d_x)
         thff.ThunderFFT_global(T, n, forward, d_x, d_lib, batch)
-        for kind in ("smem", "reg"):
+        for kind in ("smem", "reg", "smem_reversed_in"):
             d_y = torch.full_like(d_x, float("nan"))
             if kind == "smem":
                 rc = ex.thffx_device_fft(PREC[T], n, int(forward), d_x.data_ptr(), d_y.data_ptr(),
                                          batch, guard.data_ptr(), None)
+            elif kind == "smem_reversed_in":
+                # a reversed input layout: the permutation the transforms expect (identity)
+                rc = ex.thffx_device_fft_reversed_in(PREC[T], n, int(forward), d_x.data_ptr(),
+                                                     d_y.data_ptr(), batch, guard.data_ptr(), None)
             else:
                 rc = ex.thffx_device_fft_reg(PREC[T], n, int(forward), d_x.data_ptr(),
                                              d_y.data_ptr(), batch, None)

@@ -29,3 +29,30 @@ def test_header_is_self_contained(header, tmp_path):
                           "-I", os.path.join(ROOT, "include"), str(src)],
                          capture_output=True, text=True, timeout=300)
     assert res.returncode == 0, res.stderr
+
+
+def _compile(tmp_path, source):
+    src = tmp_path / "k.hip"
+    src.write_text("#include <thunderfft/thunderfft.cuh>\n" + source)
+    return subprocess.run([hipcc(), "--offload-arch=gfx950", "-std=c++17", "-fsyntax-only",
+                           "-I", os.path.join(ROOT, "include"), str(src)],
+                          capture_output=True, text=True, timeout=300)
+
+
+def test_reversed_layouts(tmp_path):
+    """layout_t's Reversed flag (reference thunderfft.cuh:29-44): accepted on
+    an input layout (the permutation the transforms expect, the identity
+    here); an output layout must not be reversed, as in the reference
+    (thunderfft_impl_helper.cuh:51-56), which is a compile-time error here."""
+    reversed_l = "using L = thunderfft::layout_t<256, 16, 1, 272, 16, 1, true>;\n"
+    ok = _compile(tmp_path, reversed_l +
+                  "static_assert(L::reversed && L::at(3, 1) == 3 + 272 + (275 / 16));\n"
+                  "__global__ void k(const __half2* in) {\n"
+                  "  __shared__ __half2 s[16 * 289];\n"
+                  "  thunderfft::ThunderFFT_gmem2smem<half, L>(s, in);\n}\n")
+    assert ok.returncode == 0, ok.stderr
+    bad = _compile(tmp_path, reversed_l +
+                   "__global__ void k(__half2* out) {\n"
+                   "  __shared__ __half2 s[16 * 289];\n"
+                   "  thunderfft::ThunderFFT_smem2gmem<half, L>(out, s);\n}\n")
+    assert bad.returncode != 0 and "must not be reversed" in bad.stderr

@@ -9,6 +9,8 @@
 //   thffx_device_fft_reg  the same through ThunderFFT_gmem2reg / reg2gmem only;
 //   thffx_fused_filter    forward FFT x per-bin filter x inverse FFT / N in one
 //                         kernel (the reference's fused-convolution pattern);
+//   thffx_device_fft_reversed_in
+//                         thffx_device_fft with a Reversed = true input layout;
 //   thffx_device_fft_w, thffx_fused_filter_w
 //                         the same two with ThunderFFT_kernel_reg(reg, W, ws) in
 //                         the reference's argument types: for half, W from
@@ -25,11 +27,15 @@ namespace {
 constexpr int kGuard = 64;
 constexpr float kGuardRe = 299.f, kGuardIm = -299.f;
 
-template <class T, int N, bool FWD>
+// kReversedIn: the input is staged through a layout_t with Reversed = true
+// (a reference fused kernel's input layout), the output through the same
+// layout with Reversed = false.
+template <class T, int N, bool FWD, bool kReversedIn = false>
 __global__ __launch_bounds__(256) void device_fft(const vec2_t<T>* in, vec2_t<T>* out,
                                                   const float2* tw, int* guard_changes) {
     constexpr int BPB = thunderfft::batch_per_block<N>;
     using L = thunderfft::layout_t<N, BPB, 1, N + thunderfft::pad_h(N), 16, 1, false>;
+    using Lin = thunderfft::layout_t<N, BPB, 1, N + thunderfft::pad_h(N), 16, 1, kReversedIn>;
     constexpr int kWorkBytes = thunderfft::workspace_bytes<N, BPB>;
     // The staging tile (L) and the FFT workspace share one LDS buffer.
     constexpr int kStageBytes = (L::at(N - 1, BPB - 1) + 1) * sizeof(vec2_t<T>);
@@ -43,9 +49,9 @@ __global__ __launch_bounds__(256) void device_fft(const vec2_t<T>* in, vec2_t<T>
     thunderfft::lane_twiddles<N> w;
     thunderfft::ThunderFFT_load_twiddles<N>(w, tw);
     vec2_t<T> reg[thunderfft::elements_per_thread];
-    thunderfft::ThunderFFT_gmem2smem<T, L>(stage, in + blockIdx.x * BPB * N);
+    thunderfft::ThunderFFT_gmem2smem<T, Lin>(stage, in + blockIdx.x * BPB * N);
     __syncthreads();
-    thunderfft::ThunderFFT_smem2reg<T, L>(reg, stage);
+    thunderfft::ThunderFFT_smem2reg<T, Lin>(reg, stage);
     __syncthreads();
     thunderfft::ThunderFFT_kernel_reg<T, N, BPB, FWD>(reg, w, raw);
     __syncthreads();
@@ -203,6 +209,9 @@ int launch(int kind, int forward, const void* x, void* y, const void* H, int bat
         else device_fft_reg<T, N, false><<<grid, 256, 0, s>>>(in, out, tw);
     } else if (kind == 2) {
         fused_filter<T, N><<<grid, 256, 0, s>>>(in, out, static_cast<const float2*>(H), tw);
+    } else if (kind == 5) {
+        if (forward) device_fft<T, N, true, true><<<grid, 256, 0, s>>>(in, out, tw, guard);
+        else device_fft<T, N, false, true><<<grid, 256, 0, s>>>(in, out, tw, guard);
     } else if (kind == 3) {
         if (forward) device_fft_w<T, N, true><<<grid, 256, 0, s>>>(in, out, tw);
         else device_fft_w<T, N, false><<<grid, 256, 0, s>>>(in, out, tw);
@@ -229,7 +238,9 @@ int dispatch(int n, int kind, int forward, const void* x, void* y, const void* H
 
 int run(int precision, int n, int kind, int forward, const void* x, void* y, const void* H,
         int batch, int* guard, void* stream) {
-    if (!x || !y || x == y || (kind == 0 && !guard) || ((kind == 2 || kind == 4) && !H)) return -22;
+    if (!x || !y || x == y || ((kind == 0 || kind == 5) && !guard) ||
+        ((kind == 2 || kind == 4) && !H))
+        return -22;
     const void* table = nullptr;
     int tn = 0;
     if (thff_twiddle_info(precision, &table, &tn) != 0 || tn != n || !table) return -22;
@@ -260,6 +271,10 @@ int thffx_device_fft_reg(int precision, int n, int forward, const void* x, void*
 int thffx_fused_filter(int precision, int n, const void* x, void* y, const void* d_filter,
                        int batch, void* stream) {
     return run(precision, n, 2, 1, x, y, d_filter, batch, nullptr, stream);
+}
+int thffx_device_fft_reversed_in(int precision, int n, int forward, const void* x, void* y,
+                                 int batch, int* d_guard_changes, void* stream) {
+    return run(precision, n, 5, forward, x, y, nullptr, batch, d_guard_changes, stream);
 }
 int thffx_device_fft_w(int precision, int n, int forward, const void* x, void* y, int batch,
                        void* stream) {
