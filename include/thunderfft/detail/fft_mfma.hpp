@@ -558,7 +558,7 @@ namespace thff {
 //             + ((t1 + k1) & 3).  Writers (fixed b, r) have t0 = 4 (n & 3) + b,
 //             t1 = 4 w + (n >> 2), k1 = q + 4 r: banks 16 (b + q) + 4 ((w + n) & 3)
 //             + (((n >> 2) + q) & 3) mod 64, all different.
-//   output staging: out_pad(k) = k + (k >> 6), conflict-free for the stage-3 writes.
+//   output staging: in 16-byte chunks, out_chunk (conflict-free 16-byte writes and reads).
 // Three workgroup barriers per tile.  The data is rounded to f16 before stages
 // 2 and 3, as in the two-stage kernel.
 // ---------------------------------------------------------------------------
@@ -566,8 +566,16 @@ struct Mfma4096 {
     static constexpr int N = 4096;
     static constexpr int kMatrix = 272;             // exchange matrix stride (dwords)
     static constexpr int kExchange = 16 * kMatrix;  // 4352
-    static constexpr int kOut = 4096 + 64;          // >= out_pad(4095) + 1 = 4159
-    __device__ static __forceinline__ int out_pad(int k) { return k + (k >> 6); }
+    static constexpr int kOut = 4096;               // output staging (dwords)
+    // Output staging: value k sits in slot k & 3 of the 16-byte chunk
+    // out_chunk(k >> 2), chunk K at position K ^ ((K >> 4) & 3).  Lane (n, q)
+    // of wave w writes its four blocks' values 4 w + b + 16 n + 256 k3
+    // (b = 0..3) as one chunk K = w + 4 n + 64 k3; over 16 lanes of one
+    // q the positions mod 16 are (w + 4 (n & 3)) ^ (n >> 2), all different.
+    // Lane t reads the chunks t + 256 i, 16 consecutive chunks (same K >> 4)
+    // per 16 lanes, also all different: both sides are conflict-free
+    // 16-byte accesses.
+    __device__ static __forceinline__ int out_chunk(int K) { return K ^ ((K >> 4) & 3); }
 };
 
 // Exchange element (k1, t0, t1) sits at 272 k1 + 16 t0 + 4 (((t1 >> 2) +
@@ -799,20 +807,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
             // the lane's 4 consecutive outputs straight to HBM instead leaves each
             // 64-byte segment to four waves and measured 4x slower.)
 #pragma unroll
-            for (int b = 0; b < 4; ++b)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    obuf[P::out_pad(4 * wave + b + 16 * n + 256 * (q + 4 * r))] =
-                        pack_half2(y[b][r]);
+            for (int r = 0; r < 4; ++r)
+                reinterpret_cast<u32x4*>(obuf)[P::out_chunk(wave + 4 * n + 64 * (q + 4 * r))] =
+                    u32x4{pack_half2(y[0][r]), pack_half2(y[1][r]), pack_half2(y[2][r]),
+                          pack_half2(y[3][r])};
             __syncthreads();
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int e = 4 * tid + 1024 * i;
-                u32x4 v;
-#pragma unroll
-                for (int c = 0; c < 4; ++c) v[c] = obuf[P::out_pad(e + c)];
-                st_nt(reinterpret_cast<u32x4*>(dst + e), v);
-            }
+            for (int i = 0; i < 4; ++i)
+                st_nt(reinterpret_cast<u32x4*>(dst + 4 * tid + 1024 * i),
+                      reinterpret_cast<const u32x4*>(obuf)[P::out_chunk(tid + 256 * i)]);
         }
     }
 }
