@@ -277,11 +277,10 @@ def time_conv_valid(T: str, ntaps: int, steps: int, warmup: int) -> dict:
     ms = timed(launch, steps, warmup, stream)
     thff.ThunderFFTFinalize(T)
     nbytes = (length + out_len) * elem
-    win = 256 if T == "half" else 64
+    win = 256 if T == "half" else 64  # half: 256-point windows on MFMA; float: 64-point on VALU
     windows = -(-out_len // (win + 1 - ntaps))
     flops = windows * (2 * 5.0 * win * math.log2(win) + 6.0 * win)
     del x, y, taps
-    win = 256 if T == "half" else 64  # half: 256-point windows on MFMA; float: 64-point on VALU
     return {"workload": (f"conv1d_valid {length} x {ntaps} taps {T}2, {win}-point windows "
                          f"({win + 1 - ntaps} outputs each)"),
             "precision": T, "us_per_call": ms * 1e3, "median_us_per_call": LAST_MEDIAN_MS * 1e3,
