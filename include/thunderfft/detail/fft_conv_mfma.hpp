@@ -49,23 +49,27 @@ __device__ __forceinline__ void split_rows(u32x4 lo, u32x4 hi, u32x4& r0, u32x4&
 // Real-input fused convolution (conv1d_real_kernel's contract, fp16 storage)
 // on MFMA: complex transform tau = p * D + d carries rows (2p, d) and
 // (2p + 1, d) as real and imaginary parts; a wave owns kFPW = 4/C transforms
-// (1024 complex values), a tile is 4 waves.  Lane l moves 8 values of both
-// rows per 16-byte step: values e = 8 l + 512 i (i = 0, 1) of the wave.
-// The spectra of a wave's transforms are kept in fp32 registers across tiles
-// (reloaded when the channels change), which holds C = 1 (four transforms per
-// wave, each with its own channel) to 2 waves per SIMD and the others to 3.
+// (1024 complex values) for C <= 4 and one of 2048 for C = 8, a tile is 4
+// waves.  Lane l moves 8 values of both rows per 16-byte step: values
+// e = 8 l + 512 i (i < kSteps) of the wave.  For C <= 4 the spectra of a
+// wave's transforms are kept in fp32 registers across tiles (reloaded when
+// the channels change), which holds C = 1 (four transforms per wave, each
+// with its own channel) to 2 waves per SIMD and the others to 3.  At C = 8
+// the transform's 32 values per lane leave no registers for them: the
+// product reads the channel's spectrum (fp32, L2-resident) per tile.
 template <int C>
-inline constexpr int kConvMfmaMinWavesPerEU = C == 1 ? 2 : 3;
+inline constexpr int kConvMfmaMinWavesPerEU = C == 1 || C == 8 ? 2 : 3;
 
 template <int C>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kConvMfmaMinWavesPerEU<C>))) void
 conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__ spectrum,
                         __half* __restrict__ y, int batch, int channels,
                         const float2* __restrict__ tw, int tiles_per_block) {
-    static_assert(C <= 4, "one 1024-value wave span per tile step");
     using P = MfmaPlan<C>;
     constexpr int N = P::N;
     constexpr int kB = P::kBlocks;
+    constexpr int kSteps = P::kWaveVals / 512;  // 16-byte steps of 8 values per lane
+    constexpr bool kKeepSpectra = C <= 4;
     __shared__ unsigned lds[4 * P::kRegion];
     __shared__ cpx w1[P::kTw1];
     __shared__ u32x4 a3[P::kA3];
@@ -85,14 +89,14 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
     long long tile, tile_end, step;
     tile_walk(ntiles, tiles_per_block, tile, tile_end, step);
     int spec_d = -1;  // chan[0] of the spectra spec holds
-    cpx spec[kB][4];
+    cpx spec[kKeepSpectra ? kB : 1][4];
 
     for (; tile < tile_end; tile += step) {
         // Rows of this wave's transforms, as element offsets (-1: none).
-        long long base0[2], base1[2];
+        long long base0[kSteps], base1[kSteps];
         int chan[P::kFPW];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kSteps; ++i) {
             const int e = 8 * lane + 512 * i;
             const long long tau = tile * P::kFPB + wave * P::kFPW + e / N;
             const long long p = tau / channels, d = tau - p * channels;
@@ -105,15 +109,15 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
 #pragma unroll
         for (int f = 0; f < P::kFPW; ++f)
             chan[f] = static_cast<int>((tile * P::kFPB + wave * P::kFPW + f) % channels);
-        u32x4 r0[2], r1[2];
+        u32x4 r0[kSteps], r1[kSteps];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kSteps; ++i) {
             r0[i] = base0[i] >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + base0[i])) : u32x4{};
             r1[i] = base1[i] >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + base1[i])) : u32x4{};
         }
         wave_lds_sync();  // the previous tile's output reads are done
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kSteps; ++i) {
             const int e = 8 * lane + 512 * i;
             u32x4 lo, hi;
             interleave_rows(r0[i], r1[i], lo, hi);
@@ -130,7 +134,25 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
         // channels do not change: they are chan[0] + f mod D, so chan[0]
         // decides, and on a grid-stride walk whose stride in transforms is a
         // multiple of D it never changes.
-        if (chan[0] != spec_d) {
+        if constexpr (kKeepSpectra) {
+            if (chan[0] != spec_d) {
+#pragma unroll
+                for (int b = 0; b < kB; ++b) {
+                    const float2* hs = spectrum + static_cast<long long>(chan[b / C]) * N + n +
+                                       16 * (b % C) + P::kM * q;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float2 hk = hs[P::kM * 4 * r];
+                        spec[b][r] = cpx{hk.x, hk.y};
+                    }
+                }
+                spec_d = chan[0];
+            }
+#pragma unroll
+            for (int b = 0; b < kB; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], spec[b][r]);
+        } else {
 #pragma unroll
             for (int b = 0; b < kB; ++b) {
                 const float2* hs = spectrum + static_cast<long long>(chan[b / C]) * N + n +
@@ -138,15 +160,10 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float2 hk = hs[P::kM * 4 * r];
-                    spec[b][r] = cpx{hk.x, hk.y};
+                    v[b][r] = cmul(v[b][r], cpx{hk.x, hk.y});
                 }
             }
-            spec_d = chan[0];
         }
-#pragma unroll
-        for (int b = 0; b < kB; ++b)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], spec[b][r]);
         // ---- inverse = conj(DFT(conj(product))), stage 1 straight from the registers ----
         mfma_stage1_regs<C, true>(a_regs, v);
         mfma_steps2to6<C, true>(region, w1, s3, lane, v);
@@ -160,7 +177,7 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
                     pack_half2({v[b][r].re, -v[b][r].im});
         wave_lds_sync();
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kSteps; ++i) {
             const int e = 8 * lane + 512 * i;
             const u32x4 lo = *reinterpret_cast<const u32x4*>(region + P::out_pad(e));
             const u32x4 hi = *reinterpret_cast<const u32x4*>(region + P::out_pad(e + 4));

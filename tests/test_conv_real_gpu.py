@@ -229,7 +229,7 @@ def test_full_size_impulse_rolls(T, n, batch, channels):
         # fp32 between the transforms: every element within fp32 rounding
         assert np.all(err <= 1e-5 * np.abs(expect) + 2e-6), label
     else:
-        # fp16 N = 256 ... 1024 run on MFMA with f16 data between the stages:
+        # fp16 N >= 256 run on MFMA with f16 data between the stages:
         # errors are spread evenly over a signal, so bound them against the
         # signal scale (|x| <= 1 here); a wrong shift or channel is O(1)
         assert rel <= 1e-3 and err.max() <= 5e-3, label

@@ -177,9 +177,8 @@ hipError_t launch_c2c(int precision, bool forward, bool aligned16, const void* i
 //   real fp32: 2 per CU with prefetch, late up to N = 512 and early above:
 //     97-116 us for N = 64 ... 512 (one tile per workgroup 110-153) and
 //     112/121/115 us for N = 1024/2048/4096 (168-176 without prefetch).
-//   fp16 on VALU (N = 64, 128; real also N = 2048, complex N <= 128 only):
-//     real 4 per CU (62-64 us; prefetch 62-74) and 3 at N = 2048 (102 us;
-//     prefetch 124), complex 16 per CU (conv1d 78-87 us against 85-91).
+//   fp16 on VALU (N = 64, 128 only): real 4 per CU (62-64 us; prefetch
+//     62-74), complex 16 per CU (conv1d 78-87 us against 85-91).
 struct ConvShape {
     int per_cu;
     Prefetch prefetch;
@@ -187,7 +186,7 @@ struct ConvShape {
 
 template <int N>
 constexpr ConvShape valu_conv_shape(int precision, bool real, bool per_signal) {
-    if (precision != 0) return {real ? (N == 2048 ? 3 : 4) : 16, Prefetch::kNone};
+    if (precision != 0) return {real ? 4 : 16, Prefetch::kNone};
     if (real) return {2, N <= 512 ? Prefetch::kLate : Prefetch::kEarly};
     if (per_signal) return {N <= 1024 ? 0 : N == 2048 ? 3 : 2, Prefetch::kNone};
     if (N <= 256) return {0, Prefetch::kNone};
@@ -284,16 +283,16 @@ hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectr
                               hipStream_t stream) {
     using P = C2CPlan<N>;
     const long long transforms = (static_cast<long long>(batch) + 1) / 2 * channels;
-    // fp16 N = 256 ... 1024: both transforms on MFMA (fft_conv_mfma.hpp);
+    // fp16 N = 256 ... 2048: both transforms on MFMA (fft_conv_mfma.hpp);
     // measured against this VALU path at 2^26 samples: 61 vs 68 us (N=256),
     // 60 vs 87 (512), 64 vs 87 (1024).  Grid: the occupancy (2 workgroups per
-    // CU for N = 256, else 3); the channels' spectra stay in registers
-    // (5-9% over reloading them per tile).
-    if constexpr (N >= 256 && N <= 1024) {
+    // CU for N = 256 and 2048, else 3); up to N = 1024 the channels' spectra
+    // stay in registers (5-9% over reloading them per tile).
+    if constexpr (N >= 256 && N <= 2048) {
         if (precision != 0) {
             using M = MfmaPlan<N / 256>;
             const long long ntiles = (transforms + M::kFPB - 1) / M::kFPB;
-            const Grid g = make_grid(ntiles, N == 256 ? 2 : 3, num_cus);
+            const Grid g = make_grid(ntiles, N == 256 || N == 2048 ? 2 : 3, num_cus);
             conv1d_real_mfma_kernel<N / 256><<<g.blocks, 256, 0, stream>>>(
                 static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch, channels,
                 tw, g.tiles_per_block);
