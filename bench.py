@@ -423,16 +423,25 @@ def cpu_baseline(target_s: float) -> dict:
 
 
 def cpu_model() -> str:
-    """The host CPU's model name (/proc/cpuinfo), or the platform string."""
+    """The host CPU's model name with its family / model / stepping numbers
+    (/proc/cpuinfo; a virtual machine may report only a generic name such as
+    "AMD EPYC"), or the platform string."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break  # the first processor's block is enough
+                key, _, value = line.partition(":")
+                fields[key.strip()] = value.strip()
     except OSError:
         pass
-    import platform
-    return platform.processor() or platform.machine()
+    name = fields.get("model name")
+    if not name:
+        import platform
+        return platform.processor() or platform.machine()
+    ids = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+    return f"{name} ({', '.join(ids)})" if ids else name
 
 
 def sync_wrapper(T: str, calls: int = 25, warmup: int = 10) -> dict:
