@@ -120,3 +120,73 @@ def test_conv_async_on_stream():
     thff.ThunderFFT_conv1d_async("half", n, d_x, d_h, y, batch, True, s)
     s.synchronize()
     assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+
+
+def test_initialize_races_transforms_on_another_thread():
+    """The transform path takes no lock (it reads the registry with atomic
+    loads) and Initialize keeps a replaced table allocated: while one host
+    thread switches the current float length between 1024 and 512, another
+    runs N=1024 transforms on its own stream.  Each call either returns the
+    bit-exact result of an undisturbed call or fails with the documented
+    missing-table error; none crashes or reads a freed table."""
+    import threading
+
+    import torch
+
+    import thunderfft_amd as thff
+
+    n, batch, calls = 1024, 64, 150
+    thff.ThunderFFTInitialize("float", n)
+    x = oracle.uniform(n, batch, seed=11)
+    d_x = to_device(x, "float")
+    d_ref = torch.empty_like(d_x)
+    thff.ThunderFFT_global("float", n, True, d_x, d_ref, batch)
+    ref = from_device(d_ref, "float")
+    m = oracle.metrics(ref.reshape(batch, n), oracle.fft(x, True))
+    assert m["rel_l2"] <= TIGHT["float"], m
+
+    stream = torch.cuda.Stream()
+    outcome = {"ok": 0, "missing": 0, "mismatch": 0, "other": [], "switches": 0}
+    start = threading.Barrier(2)
+    done = threading.Event()
+
+    def transforms():
+        d_y = torch.empty_like(d_x)
+        start.wait()
+        for _ in range(calls):
+            d_y.fill_(float("nan"))
+            torch.cuda.synchronize()
+            try:
+                thff.ThunderFFT_global("float", n, True, d_x, d_y, batch, stream)
+            except RuntimeError as e:
+                if "ThunderFFTInitialize" in str(e):
+                    outcome["missing"] += 1
+                else:
+                    outcome["other"].append(str(e))
+                continue
+            if torch.equal(d_y, d_ref):
+                outcome["ok"] += 1
+            else:
+                outcome["mismatch"] += 1
+        done.set()
+
+    def switches():
+        start.wait()
+        while not done.is_set():  # toggle for as long as the transforms run
+            thff.ThunderFFTInitialize("float", 512)
+            thff.ThunderFFTInitialize("float", n)
+            outcome["switches"] += 1
+
+    workers = [threading.Thread(target=transforms), threading.Thread(target=switches)]
+    for w in workers:
+        w.start()
+    for w in workers:
+        w.join()
+    print(f"initialize race: {outcome}", flush=True)
+    assert outcome["mismatch"] == 0 and not outcome["other"], outcome
+    assert outcome["ok"] + outcome["missing"] == calls, outcome
+    # the replaced tables stayed allocated: N=1024 is still served afterwards
+    thff.ThunderFFTInitialize("float", n)
+    d_y = torch.empty_like(d_x)
+    thff.ThunderFFT_global("float", n, True, d_x, d_y, batch)
+    assert torch.equal(d_y, d_ref)
