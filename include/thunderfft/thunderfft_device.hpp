@@ -274,9 +274,18 @@ inline constexpr int coefficient_count =
 // operands and every twiddle the transform needs, computed with the hardware
 // transcendentals (no table, no memory access; their error is far below the
 // f16 rounding of the data), once per kernel.  Call with the same block
-// shape and lane numbering as ThunderFFT_kernel_reg.
-template <int N, bool forward>
-__device__ __forceinline__ void make_reg_b_precompute(vec2_t<half>* W) {
+// shape and lane numbering as ThunderFFT_kernel_reg.  W is a vec2_t<half>
+// array or pointer; an array is checked at compile time to hold
+// coefficient_count<N> slots (the reference's kernels declare 28 or 36,
+// fewer than the MFMA transforms at N = 1024 and 4096 need).
+template <int N, bool forward, class Coeffs>
+__device__ __forceinline__ void make_reg_b_precompute(Coeffs&& W_arg) {
+    using A = std::remove_reference_t<Coeffs>;
+    if constexpr (std::is_array_v<A>)
+        static_assert(std::extent_v<A> >= static_cast<size_t>(coefficient_count<N>),
+                      "make_reg_b_precompute: declare vec2_t<half> "
+                      "W[thunderfft::unit_fp16::coefficient_count<N>]");
+    vec2_t<half>* const W = W_arg;
     detail::check_shape<N, batch_per_block<N>>();
     const int tid = detail::block_tid();
     detail::half_coefficients<N> k;

@@ -56,3 +56,23 @@ def test_reversed_layouts(tmp_path):
                    "  __shared__ __half2 s[16 * 289];\n"
                    "  thunderfft::ThunderFFT_smem2gmem<half, L>(out, s);\n}\n")
     assert bad.returncode != 0 and "must not be reversed" in bad.stderr
+
+
+def test_precomputed_coefficients_array_size(tmp_path):
+    """unit_fp16::make_reg_b_precompute (reference unit_kernel_fp16.cuh:97-108)
+    writes coefficient_count<N> half2 slots: an array argument is checked at
+    compile time, so a reference kernel's W[36] at N = 1024 (more slots are
+    needed there) fails to compile instead of being overrun; a right-sized
+    array and a pointer compile."""
+    body = ("__global__ void k(const __half2* p) {{\n"
+            "  vec2_t<half> W[{size}];\n"
+            "  thunderfft::unit_fp16::make_reg_b_precompute<1024, true>({arg});\n"
+            "  (void)p;\n}}\n")
+    ok = _compile(tmp_path, body.format(
+        size="thunderfft::unit_fp16::coefficient_count<1024>", arg="W"))
+    assert ok.returncode == 0, ok.stderr
+    ptr = _compile(tmp_path, body.format(
+        size="thunderfft::unit_fp16::coefficient_count<1024>", arg="static_cast<vec2_t<half>*>(W)"))
+    assert ptr.returncode == 0, ptr.stderr
+    small = _compile(tmp_path, body.format(size="36", arg="W"))
+    assert small.returncode != 0 and "coefficient_count" in small.stderr, small.stderr
