@@ -300,7 +300,7 @@ def test_config5_conv2d_64x64():
     y = torch.empty_like(x)
     thff.ThunderFFTInitialize(T, 64)
 
-    # (1) the config-5 filter on a subset of images against the direct convolution
+    # (1) the benchmark filter (7 x 7 corner block) on a subset of images against the direct convolution
     h = _filter2d(5)
     thff.ThunderFFT_conv2d(T, 64, 64, x, to_device(h, T), y, batch)
     rows = np.array([0, 1, 2047, 4096, 6000, batch - 2, batch - 1])
