@@ -300,9 +300,14 @@ int conv1d_valid_impl(int precision, const void* x, long long input_len, const v
     if ((reinterpret_cast<std::uintptr_t>(x) | reinterpret_cast<std::uintptr_t>(y)) % elem ||
         reinterpret_cast<std::uintptr_t>(taps) % 8)
         return fail(THFF_EINVAL, "ThunderFFT_conv1d_valid: misaligned pointer");
-    const long long valid = 65 - filter_len;
+    // Window groups of one launch (fp32: 64 windows of 64 points per group;
+    // fp16: 16 windows of 256 points), counted in 32 bits by the kernels'
+    // grid walk.
+    const long long window = precision == THFF_FLOAT ? 64 : 256;
+    const long long per_group = precision == THFF_FLOAT ? 64 : 16;
+    const long long valid = window + 1 - filter_len;
     const long long windows = (input_len - filter_len + 1 + valid - 1) / valid;
-    if ((windows + 63) / 64 * batch * 256 > static_cast<long long>(UINT32_MAX))
+    if ((windows + per_group - 1) / per_group * batch * 256 > static_cast<long long>(UINT32_MAX))
         return fail(THFF_EINVAL, "ThunderFFT batch exceeds one launch for this length");
     const float2* table = nullptr;
     int cus = 0;
