@@ -874,3 +874,271 @@ conv1d_valid_mfma_kernel(const __half2* __restrict__ x, const float2* __restrict
 }
 
 }  // namespace thff
+
+namespace thff {
+
+// ---------------------------------------------------------------------------
+// half2 2-D convolution of 64 x 64 images on MFMA (conv2d64_kernel's contract:
+// y = IFFT2(FFT2(x) * FFT2(h)) / 4096, one shared filter), one image per
+// workgroup tile.  Both 64-point transforms of the 2-D DFT split as 64 = 16 x 4:
+// a DFT16 on v_mfma_f32_16x16x32_f16 over the stride-4 index, the twiddle
+// W64^(j k), then an in-lane DFT4.  With lane (n, q) (lane = n + 16 q) of wave w:
+//   F1 columns: wave w owns the 16 columns c = 16 w + n; block b = r0 holds the
+//      DFT16 inputs r1 = 4 q + e (row r = r0 + 4 r1) from the staged image; the
+//      grouped operands (dft16_operands_grouped) leave kr1 = 4 q + t in t, so
+//      after W64^(r0 kr1) and the DFT4 over r0 the lane holds
+//      Xc[kr = 4 q + t + 16 kr0][c], four consecutive rows per kr0.
+//   exchange (LDS, column-major, 16-byte writes) to rows: wave w owns the rows
+//      kr = 16 w + n; block c0 holds inputs c1 = 4 q + e (c = c0 + 4 c1).
+//   F2 rows: DFT16 (grouped outputs kc1 = 4 q + t), W64^(c0 kc1), DFT4 over c0
+//      -> spectrum X[kr = 16 w + n][kc = 4 q + t + 16 kc0], the filter's alike.
+// The inverse is conj(DFT2(conj(P))), rows first, straight from the spectrum:
+// kc = kc1 + 16 kc0 gives the DFT4 over kc0 in-lane first, W64^(kc1 k1), then
+// the DFT16 over kc1 (whose lane group q already holds kc1 = 4 q + t) -> column
+// c = k1 + 16 q + 4 r; an exchange (row-major, 16-byte writes) back to columns
+// with rows kr = 4 q + e + 16 n2 per lane: DFT4 over n2, W64^((4 q + e) k1),
+// DFT16 over n1 = 4 q + e (plain q + 4 r outputs) -> row k1 + 4 q + 16 r, staged
+// for 16-byte stores.  Every twiddle multiplies a DFT16's outputs (F1, F2) or
+// inputs (the inverse) in block j = 1..3, so it is folded into that block's
+// DFT16 operands: output k, input i of the complex coefficient matrix become
+// W64^(k (j + 4 i)) (outputs twiddled) or W64^(i (4 k + j)) (inputs
+// twiddled), rounded to f16 like the data at that stage.  Block 0 uses the
+// plain operands; the 18 other operand sets (3 forms x 3 blocks x 2 halves)
+// are built once per workgroup into an LDS table.  f16 data enters each DFT16,
+// fp32 elsewhere; the filter spectrum (x 1/4096) stays in fp32 registers.  Two
+// LDS buffers alternate, so an image takes four workgroup barriers.
+// Bank-conflict-free layouts (dword units):
+//   input staging  (r, c) at r 64 + c + 16 (r >> 4)
+//   forward exchange (kr, c) at c 68 + (kr ^ 16 (c >> 4))
+//   inverse exchange and output staging (r, c) at r 68 + c
+// ---------------------------------------------------------------------------
+namespace conv2dm {
+constexpr int kStride = 68;
+constexpr int kBuf = 64 * kStride;  // dwords per buffer (>= every layout's extent)
+__device__ __forceinline__ int in_addr(int r, int c) { return r * 64 + c + 16 * (r >> 4); }
+__device__ __forceinline__ int fx_addr(int kr, int c) {
+    return c * kStride + (kr ^ (16 * (c >> 4)));
+}
+__device__ __forceinline__ int rm_addr(int r, int c) { return r * kStride + c; }
+
+__device__ __forceinline__ cpx unpack_half2(unsigned w) {
+    const float2 f = __half22float2(__builtin_bit_cast(__half2, w));
+    return {f.x, f.y};
+}
+
+// DFT4 over the block index of v[b][t] for every t (in-lane), forward.
+__device__ __forceinline__ void dft4_blocks(cpx (&v)[4][4]) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        cpx u[4] = {v[0][t], v[1][t], v[2][t], v[3][t]};
+        Dft<4, true>::run(u);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k][t] = u[k];
+    }
+}
+
+// Operand table: form f (0: outputs twiddled, grouped outputs -- F1, F2;
+// 1: inputs twiddled, grouped outputs -- inverse rows; 2: inputs twiddled,
+// q + 4 r outputs -- inverse columns), block j = 1..3, half h, lane.
+constexpr int kForms = 3;
+constexpr int kOps = kForms * 3 * 2 * 64;  // u32x4 entries (18 KB)
+__device__ __forceinline__ int op_index(int form, int j, int h, int lane) {
+    return ((form * 3 + (j - 1)) * 2 + h) * 64 + lane;
+}
+
+// Entry e of the table, from the positive-angle table of length 64 (forward
+// sign: the conjugate).  Row m of half h is output k (grouped: 4 (m/4) + 2 h +
+// (m%4)/2; q + 4 r order: m/4 + 4 (2 h + (m%4)/2)), part (m%4)%2; column kk is
+// input i = kk/2, part kk%2.
+__device__ __forceinline__ u32x4 op_entry(int e, const float2* __restrict__ tw64) {
+    const int lane = e & 63, h = (e >> 6) & 1, j = (e >> 7) % 3 + 1, form = (e >> 7) / 3;
+    const int m = lane & 15, kq = lane >> 4;
+    const int gq = m >> 2, i2 = m & 3, o = i2 & 1;
+    const int k = form == 2 ? gq + 4 * (2 * h + (i2 >> 1)) : 4 * gq + 2 * h + (i2 >> 1);
+    f16x8 r;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+        const int kk = 8 * kq + x;
+        const int in = kk >> 1, p = kk & 1;
+        const int idx = form == 0 ? k * (j + 4 * in) : in * (4 * k + j);
+        const float2 w = tw64[idx & 63];
+        const float c = w.x, sn = -w.y;
+        // out.re = c*in.re - s*in.im ; out.im = s*in.re + c*in.im
+        const float v = o == 0 ? (p == 0 ? c : -sn) : (p == 0 ? sn : c);
+        r[x] = static_cast<_Float16>(v);
+    }
+    return __builtin_bit_cast(u32x4, r);
+}
+
+// Operands of block b of a stage of form `form`: the plain ones for b = 0.
+__device__ __forceinline__ void stage_ops(const u32x4* ops, const f16x8 (&plain)[2], int form,
+                                          int b, int lane, f16x8 (&op)[2]) {
+    if (b == 0) {
+        op[0] = plain[0];
+        op[1] = plain[1];
+    } else {
+        op[0] = __builtin_bit_cast(f16x8, ops[op_index(form, b, 0, lane)]);
+        op[1] = __builtin_bit_cast(f16x8, ops[op_index(form, b, 1, lane)]);
+    }
+}
+
+// The 2-D forward transform of the image staged in `in` (in_addr layout)
+// through the exchange buffer `fx` -> spectrum v[kc0][t] of row 16 w + n,
+// column 4 q + t + 16 kc0.  `fx` is written without a barrier before: its
+// previous readers must have passed one.  Ends after the F2 reads (fx busy).
+__device__ __forceinline__ void forward(const unsigned* in, unsigned* fx, const f16x8 (&ag)[2],
+                                        const u32x4* ops, int wave, int lane, cpx (&v)[4][4]) {
+    const int n = lane & 15, q = lane >> 4;
+    // F1: columns 16 w + n, block r0, inputs r1 = 4 q + e; W64^(r0 kr1) folded
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        u32x4 xv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[e] = in[in_addr(b + 16 * q + 4 * e, 16 * wave + n)];
+        f16x8 op[2];
+        stage_ops(ops, ag, 0, b, lane, op);
+        dft16_block(op, as_f16x8(xv), v[b]);
+    }
+    dft4_blocks(v);  // v[kr0][t]: row 4 q + t + 16 kr0
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        *reinterpret_cast<u32x4*>(fx + fx_addr(4 * q + 16 * k, 16 * wave + n)) =
+            u32x4{pack_half2(v[k][0]), pack_half2(v[k][1]), pack_half2(v[k][2]),
+                  pack_half2(v[k][3])};
+    __syncthreads();
+    // F2: rows 16 w + n, block c0, inputs c1 = 4 q + e; W64^(c0 kc1) folded
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        u32x4 xv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[e] = fx[fx_addr(16 * wave + n, b + 16 * q + 4 * e)];
+        f16x8 op[2];
+        stage_ops(ops, ag, 0, b, lane, op);
+        dft16_block(op, as_f16x8(xv), v[b]);
+    }
+    dft4_blocks(v);  // v[kc0][t]: column 4 q + t + 16 kc0
+}
+
+}  // namespace conv2dm
+
+template <int kPerCu = 3>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kPerCu))) void
+conv2d64_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
+                     __half2* __restrict__ y, int batch, const float2* __restrict__ tw64,
+                     int tiles_per_block) {
+    using namespace conv2dm;
+    __shared__ __align__(16) unsigned buf[2][kBuf];
+    __shared__ u32x4 ops[kOps];
+    unsigned* const A = buf[0];
+    unsigned* const B = buf[1];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int n = lane & 15, q = lane >> 4;
+
+    f16x8 ag[2], as[2];
+    dft16_operands_grouped<true>(ag, lane);
+    dft16_operands<true>(as, lane);
+    for (int e = tid; e < kOps; e += 256) ops[e] = op_entry(e, tw64);  // read after a barrier below
+
+    long long img, img_end, step;
+    tile_walk(batch, tiles_per_block, img, img_end, step);
+    if (img >= img_end) return;  // uniform over the workgroup
+
+    // An image's 16-byte pieces 4 tid + 1024 i, loaded and written to A.
+    auto load = [&](const __half2* src, u32x4 (&raw)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            raw[i] = ld_nt(reinterpret_cast<const u32x4*>(src + 4 * tid + 1024 * i));
+    };
+    auto stage = [&](const u32x4 (&raw)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = 4 * tid + 1024 * i;
+            *reinterpret_cast<u32x4*>(A + in_addr(f >> 6, f & 63)) = raw[i];
+        }
+    };
+
+    // The filter's spectrum / 4096, in the spectrum layout.
+    cpx hs[4][4];
+    u32x4 next[4];  // the next image's pieces, loaded while the current one is transformed
+    load(h, next);
+    stage(next);
+    load(x + img * 4096, next);
+    __syncthreads();
+    forward(A, B, ag, ops, wave, lane, hs);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) hs[k][t] = {hs[k][t].re * (1.0f / 4096), hs[k][t].im * (1.0f / 4096)};
+
+    const long long total = (img_end - img + step - 1) / step;
+    for (; img < img_end; img += step) {
+        progress_priority((img_end - img + step - 1) / step, total);
+        // A's previous readers (the filter's F1, or the last image's inverse
+        // exchange reads) passed a barrier since; B's (F2 reads) pass the one
+        // after this staging.
+        stage(next);
+        if (img + step < img_end) load(x + (img + step) * 4096, next);
+        __syncthreads();
+        cpx v[4][4];
+        forward(A, B, ag, ops, wave, lane, v);
+        // ---- product, then the inverse as conj(DFT2(conj(P))), rows first ----
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const cpx p = cmul(v[k][t], hs[k][t]);
+                v[k][t] = {p.re, -p.im};
+            }
+        dft4_blocks(v);  // over kc0 -> k1
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            u32x4 xv;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xv[t] = pack_half2(v[k][t]);  // inputs kc1 = 4 q + t
+            f16x8 op[2];
+            stage_ops(ops, ag, 1, k, lane, op);  // W64^(kc1 k1) folded
+            dft16_block(op, as_f16x8(xv), v[k]);  // v[k1][r]: column k1 + 16 q + 4 r
+        }
+        // exchange to columns (A: every wave's F1 reads passed the barrier in forward)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            *reinterpret_cast<u32x4*>(A + rm_addr(16 * wave + n, 16 * q + 4 * r)) =
+                u32x4{pack_half2(v[0][r]), pack_half2(v[1][r]), pack_half2(v[2][r]),
+                      pack_half2(v[3][r])};
+        __syncthreads();
+        // columns 16 w + n: rows n1 + 16 n2, n1 = 4 q + e
+#pragma unroll
+        for (int n2 = 0; n2 < 4; ++n2)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v[n2][e] = unpack_half2(A[rm_addr(4 * q + e + 16 * n2, 16 * wave + n)]);
+        dft4_blocks(v);  // over n2 -> k1
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            u32x4 xv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[e] = pack_half2(v[k][e]);  // inputs n1 = 4 q + e
+            f16x8 op[2];
+            stage_ops(ops, as, 2, k, lane, op);  // W64^(n1 k1) folded
+            dft16_block(op, as_f16x8(xv), v[k]);  // v[k1][r]: row k1 + 4 q + 16 r
+        }
+        // output staging in B (every wave's F2 reads passed the last barrier),
+        // conjugated back
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                B[rm_addr(k + 4 * q + 16 * r, 16 * wave + n)] = pack_half2({v[k][r].re, -v[k][r].im});
+        __syncthreads();
+        __half2* dst = y + img * 4096;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = 4 * tid + 1024 * i;
+            st_nt(reinterpret_cast<u32x4*>(dst + f),
+                  *reinterpret_cast<const u32x4*>(B + rm_addr(f >> 6, f & 63)));
+        }
+    }
+}
+
+}  // namespace thff

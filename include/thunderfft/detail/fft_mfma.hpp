@@ -82,6 +82,32 @@ __device__ __forceinline__ void dft16_operands(f16x8 (&a)[2], int lane) {
     }
 }
 
+// The DFT16 operands of dft16_operands<FWD> (plain input order) with the
+// rows permuted so that lane group q receives outputs k = 4q + r, r = 0..3
+// (four consecutive outputs) instead of q + 4r: row m of half h is output
+// k = 4 (m / 4) + 2 h + (m % 4) / 2, part (m % 4) % 2.  dft16_block then
+// leaves output 4q + r in y[r].
+template <bool FWD>
+__device__ __forceinline__ void dft16_operands_grouped(f16x8 (&a)[2], int lane) {
+    const int m = lane & 15, q = lane >> 4;
+    const int gq = m >> 2, i = m & 3;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int k = 4 * gq + 2 * h + (i >> 1);
+        const int o = i & 1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int kk = 8 * q + e;
+            const int j = kk >> 1, p = kk & 1;
+            const int ang = (j * k) & 15;
+            const float c = kCos16[ang];
+            const float s = FWD ? -kSin16[ang] : kSin16[ang];
+            const float v = o == 0 ? (p == 0 ? c : -s) : (p == 0 ? s : c);
+            a[h][e] = static_cast<_Float16>(v);
+        }
+    }
+}
+
 // Outputs r = 0..3 (k = q + 4r) of one 16-sequence DFT16 block, as complex f32.
 __device__ __forceinline__ void dft16_block(const f16x8 (&a)[2], f16x8 b, cpx* y) {
 #pragma unroll

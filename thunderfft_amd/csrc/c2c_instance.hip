@@ -362,18 +362,22 @@ hipError_t launch_conv1d_valid(int precision, const void* x, long long len, cons
 
 hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y, int batch,
                            const float2* tw, int num_cus, hipStream_t stream) {
-    // One image per tile; a device grid of 4 workgroups per CU (the kernel's
-    // occupancy) walks the images grid-stride, and each workgroup transforms
-    // the filter once.
-    const Grid g = make_grid(batch, 4, num_cus);
-    if (precision == 0)
+    // One image per tile; a device grid at the kernel's occupancy walks the
+    // images grid-stride, and each workgroup transforms the filter once.
+    // fp32: the VALU kernel, 4 workgroups per CU.  fp16: the MFMA kernel
+    // (conv2d64_mfma_kernel), kConv2dMfmaPerCu per CU.
+    if (precision == 0) {
+        const Grid g = make_grid(batch, 4, num_cus);
         conv2d64_kernel<float2><<<g.blocks, 256, 0, stream>>>(
             static_cast<const float2*>(x), static_cast<const float2*>(h), static_cast<float2*>(y),
             batch, tw, g.tiles_per_block);
-    else
-        conv2d64_kernel<__half2><<<g.blocks, 256, 0, stream>>>(
+    } else {
+        constexpr int kConv2dMfmaPerCu = 3;
+        const Grid g = make_grid(batch, kConv2dMfmaPerCu, num_cus);
+        conv2d64_mfma_kernel<kConv2dMfmaPerCu><<<g.blocks, 256, 0, stream>>>(
             static_cast<const __half2*>(x), static_cast<const __half2*>(h),
             static_cast<__half2*>(y), batch, tw, g.tiles_per_block);
+    }
     return hipGetLastError();
 }
 #endif
