@@ -633,7 +633,7 @@ def main():
                   f"{r['gflops']:.0f} GFLOP/s", file=sys.stderr, flush=True)
     thff.ThunderFFTFinalize("float")
     thff.ThunderFFTFinalize("half")
-    for kind, T in (("conv1d", "float"), ("conv1d", "half"), ("conv2d", "float")):
+    for kind, T in (("conv1d", "float"), ("conv1d", "half"), ("conv2d", "float"), ("conv2d", "half")):
         r = time_conv(kind, T, max(1, a.steps // 2), max(1, a.warmup // 2))
         runs[f"{kind}_{T}"] = r
         print(f"[bench] {r['workload']}: {r['us_per_call']:.1f} us, {r['gbps']:.0f} GB/s "
