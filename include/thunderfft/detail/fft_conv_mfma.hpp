@@ -284,13 +284,21 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
     // use, in registers that are free at that point -- the signal's while the
     // filter is transformed (its packed spectrum is not live yet), the next
     // tile's filter while the inverse runs (the spectrum is dead after the
-    // product).  1-4% faster at N = 256...1024; at C = 8 (256 VGPRs) the
-    // extra live registers spill 44 bytes per lane and it measured slower
-    // (100 vs 92-95 us), so there each load directly precedes its transform.
+    // product).  1-4% faster at N = 256...1024.  At C = 8 (256 VGPRs) only
+    // the signal's loads move ahead of the filter's transform (90-91 against
+    // 92-94 us for 16384 x 2048, same 8-byte spill); loading the next filter
+    // during the inverse as well spills 44 bytes per lane (97 us).
     constexpr bool kPipelined = kPerSignal && C <= 4;
+    // A shared filter at C <= 4: the next tile's signal loads are issued as
+    // soon as the current one is staged (its registers are free then); 1-3%
+    // faster at 2^25 values (at C = 8 the registers are not there).
+    constexpr bool kPrefetchShared = !kPerSignal && C <= 4;
     u32x4 rh[kRaw];
     if constexpr (kPipelined)
         if (tile < tile_end) load(h + offset(tile), valid(tile), rh);
+    u32x4 rn[kRaw];
+    if constexpr (kPrefetchShared)
+        if (tile < tile_end) load(x + offset(tile), valid(tile), rn);
     for (; tile < tile_end; tile += step) {
         const int nv = valid(tile);
         const long long off = offset(tile);
@@ -305,14 +313,20 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
             } else if constexpr (kPerSignal) {
                 load(h + off, nv, rh);
                 stage(rh);
+                load(x + off, nv, rx);
                 forward(v);
                 keep(v);
-                load(x + off, nv, rx);
+            } else if constexpr (kPrefetchShared) {
+                stage(rn);
+                if (tile + step < tile_end) load(x + offset(tile + step), valid(tile + step), rn);
+                forward(v);
             } else {
                 load(x + off, nv, rx);
             }
-            stage(rx);
-            forward(v);
+            if constexpr (!kPrefetchShared) {
+                stage(rx);
+                forward(v);
+            }
         }
 #pragma unroll
         for (int b = 0; b < kB; ++b)
@@ -541,7 +555,10 @@ namespace thff {
 // (a few workgroups per CU), walking the signals grid-stride (tile_walk).
 // Per-signal filters: held to 168 VGPRs (3 workgroups per CU) at the cost of a
 // 32-byte spill, 103 us against 111 us at 2 per CU (2^25 values, MI355X).  A
-// shared filter keeps its spectrum live across the loop: 2 per CU.
+// shared filter keeps its spectrum live across the loop: 2 per CU, and the
+// next signal's loads are issued before the current one's transform (64 us
+// against 73 us; for per-signal filters the extra registers spill and it
+// measured slower, 102 against 97 us).
 template <bool kPerSignal>
 inline constexpr int kConv4096MinWavesPerEU = kPerSignal ? 3 : 2;
 
@@ -606,13 +623,16 @@ conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict_
             dft16_block(op, as_f16x8(xv), v[b]);
         }
     };
-    // Forward transform of the 4096 values at src (callers: every wave done
-    // with xbuf before, as the first barrier inside requires).
-    auto forward = [&](const __half2* src, cpx (&v)[4][4]) {
-        u32x4 z[4];
+    // Stage-1 inputs of the 4096 values at src: x[64 w + 4 n + b + 256 j],
+    // j = 4 q + e, in z[e][b].
+    auto load = [&](const __half2* src, u32x4 (&z)[4]) {
         const __half2* s = src + 64 * wave + 4 * n + 1024 * q;
 #pragma unroll
         for (int e = 0; e < 4; ++e) z[e] = ld_nt(reinterpret_cast<const u32x4*>(s + 256 * e));
+    };
+    // Forward transform of loaded inputs (callers: every wave done with xbuf
+    // before, as the first barrier inside requires).
+    auto forward = [&](const u32x4 (&z)[4], cpx (&v)[4][4]) {
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             u32x4 xv;
@@ -642,18 +662,31 @@ conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict_
     long long tile, tile_end, step;
     tile_walk(batch, 0, tile, tile_end, step);
     if (tile >= tile_end) return;  // uniform over the workgroup
+    u32x4 zx[4];  // shared filter: the next signal's inputs
     if constexpr (!kPerSignal) {
         cpx v[4][4];
-        forward(h, v);
+        u32x4 zh[4];
+        load(h, zh);
+        forward(zh, v);
         keep(v);
+        load(x + tile * N, zx);
     }
     for (; tile < tile_end; tile += step) {
         cpx v[4][4];
         if constexpr (kPerSignal) {
-            forward(h + tile * N, v);
+            u32x4 z[4];
+            load(h + tile * N, z);
+            forward(z, v);
             keep(v);
+            load(x + tile * N, z);
+            forward(z, v);
+        } else {
+            u32x4 z[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) z[i] = zx[i];
+            if (tile + step < tile_end) load(x + (tile + step) * N, zx);
+            forward(z, v);
         }
-        forward(x + tile * N, v);
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
