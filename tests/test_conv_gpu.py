@@ -124,18 +124,25 @@ def test_config4_conv1d_2048(T):
     torch.cuda.empty_cache()
 
 
+# Batches with several tiles per workgroup of the device-sized grids (up to
+# 3 x 256 workgroups of 16, 4 or 1 signals at N = 256, 1024, 4096) and a
+# partial last round: exercises the loads issued a tile ahead.
+MANY = {256: 3 * 768 * 16 + 7, 1024: 3 * 768 * 4 + 3, 4096: 2112}
+
+
 @pytest.mark.parametrize("T", ["float", "half"])
 @pytest.mark.parametrize("per_signal", [True, False])
-def test_conv1d_4096_many_signals_per_workgroup(T, per_signal):
-    """2112 signals of 4096: more signals than workgroups, so every workgroup
-    convolves several in turn (a shared filter is transformed once per
-    workgroup).  A subset against the direct convolution, then every signal
-    through the impulse roll (per-signal shifts, or one shared shift)."""
+@pytest.mark.parametrize("n", sorted(MANY))
+def test_conv1d_many_signals_per_workgroup(T, per_signal, n):
+    """More signals than workgroups, so every workgroup convolves several in
+    turn (a shared filter is transformed once per workgroup or wave).  A
+    subset against the direct convolution, then every signal through the
+    impulse roll (per-signal shifts, or one shared shift)."""
     import torch
 
     import thunderfft_amd as thff
 
-    n, batch = 4096, 2112
+    batch = MANY[n]
     dt = torch.float32 if T == "float" else torch.float16
     seed = oracle.BENCH_SEED_BASE + n + 11
     x = torch.empty(2 * n * batch, dtype=dt, device="cuda")
