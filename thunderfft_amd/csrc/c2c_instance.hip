@@ -41,12 +41,12 @@ inline Grid make_grid(long long ntiles, int per_cu, int num_cus) {
 //     per workgroup: 188-194 us); with direct movement, same box: 178 / 180 us
 //     against 12 per CU 181 / 179, 8 per CU 184 / 180, 4 per CU 189 / 181,
 //     8 per CU without prefetch 186 / 186, one tile per workgroup 181 / 186.
-//   fp16 N = 2048 (MFMA): 2 per CU 93-94 us against 1 per CU 111 (with
-//     prefetch 95), 3 per CU 106, one tile per workgroup 122.
+//   fp16 N = 2048 (MFMA): 2 per CU 93-95 us against 1 per CU 111 (with
+//     prefetch 95), 3 per CU 106, one tile per workgroup 122; 2 per CU with
+//     prefetch (224 VGPRs) 102 us.
 //   fp16 N = 64, 128 (VALU): one tile per workgroup.
 //   fp16 MFMA: 2 per CU, 87-94 us (two tiles per workgroup: 87-98 us; N = 4096
-//     with contiguous shares: 99 us); N = 2048 without prefetch, which would
-//     drop the kernel to one workgroup per CU.
+//     with contiguous shares: 99 us), with prefetch except at N = 2048.
 // `direct` (VALU kernel): tiles move between HBM and the first pass's
 // registers with no LDS staging (DirectIO, fft_tile.hpp).  fp32, same box:
 // N = 256 170 vs 175 us, 512 172 vs 174, 2048 180 vs 184, 4096 179 vs 183;
