@@ -403,6 +403,42 @@ struct RealIo<__half2> {
     }
 };
 
+// Position of transform tau = p * channels + d of the real convolutions
+// (row pair p, channel d) on a tile walk whose successive tiles are `adv`
+// transforms apart: positions advance without a 64-bit division per tile,
+// and transform tau + k (k small) is located with one 32-bit division.
+struct ChannelPos {
+    long long p;
+    int d;
+};
+struct ChannelWalk {
+    long long adv_p;
+    int adv_d;
+    int channels;
+    __device__ __forceinline__ ChannelWalk(long long adv, int ch) : channels(ch) {
+        adv_p = adv / ch;
+        adv_d = static_cast<int>(adv - adv_p * ch);
+    }
+    __device__ __forceinline__ ChannelPos at(long long tau) const {
+        const long long p = tau / channels;
+        return {p, static_cast<int>(tau - p * channels)};
+    }
+    // (adv_d < channels and q.d < channels: at most one carry)
+    __device__ __forceinline__ ChannelPos advance(ChannelPos q) const {
+        q.p += adv_p;
+        q.d += adv_d;
+        if (q.d >= channels) q.d -= channels, ++q.p;
+        return q;
+    }
+    __device__ __forceinline__ void locate(ChannelPos q, int k, long long& pair, int& chan) const {
+        const unsigned s = static_cast<unsigned>(q.d) + static_cast<unsigned>(k);
+        const unsigned c = static_cast<unsigned>(channels);
+        const unsigned j = s / c;
+        pair = q.p + j;
+        chan = static_cast<int>(s - j * c);
+    }
+};
+
 // H[d][k] = scale * FFT(h[d])[k] for `channels` real fp32 filters h[d] of N
 // taps (fp32 for both storage types, so half convolutions keep exact taps).
 template <int N>
@@ -470,34 +506,12 @@ __global__ __launch_bounds__(256) void conv1d_real_kernel(
     int spec_d = -1;
     cpx spec[kKeepSpectrum ? 16 : 1];
 
-    // Position of a tile's first transform tau = tl * kFPB as pair p and
-    // channel d (tau = p * channels + d).  Successive tiles of the walk are
-    // step * kFPB = adv_p * channels + adv_d transforms apart, so positions
-    // advance without a 64-bit division per tile; transform k of a tile sits
-    // at channel (d + k) mod channels of pair p + (d + k) / channels (32-bit).
-    struct Pos {
-        long long p;
-        int d;
-    };
-    const long long adv = step * P::kFPB;
-    const long long adv_p = adv / channels;
-    const int adv_d = static_cast<int>(adv - adv_p * channels);
-    Pos pos;
-    pos.p = tile * P::kFPB / channels;
-    pos.d = static_cast<int>(tile * P::kFPB - pos.p * channels);
-    auto advance = [&](Pos q) {
-        q.p += adv_p;
-        q.d += adv_d;
-        if (q.d >= channels) q.d -= channels, ++q.p;
-        return q;
-    };
-    auto locate = [&](Pos q, int k, long long& pair, int& chan) {
-        const unsigned s = static_cast<unsigned>(q.d) + static_cast<unsigned>(k);
-        const unsigned c = static_cast<unsigned>(channels);
-        const unsigned j = s / c;
-        pair = q.p + j;
-        chan = static_cast<int>(s - j * c);
-    };
+    // Position of a tile's first transform tau = tl * kFPB (ChannelWalk).
+    using Pos = ChannelPos;
+    const ChannelWalk walk(step * P::kFPB, channels);
+    Pos pos = walk.at(tile * P::kFPB);
+    auto advance = [&](Pos q) { return walk.advance(q); };
+    auto locate = [&](Pos q, int k, long long& pair, int& chan) { walk.locate(q, k, pair, chan); };
 
     // This lane's kSteps 16-byte pieces of tile tl in both rows.  Piece i is
     // tile element e = u_i + kVec lane, u_i = 1024 wave + 64 kVec i: element

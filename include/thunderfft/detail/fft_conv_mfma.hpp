@@ -90,6 +90,9 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
     tile_walk(ntiles, tiles_per_block, tile, tile_end, step);
     int spec_d = -1;  // chan[0] of the spectra spec holds
     cpx spec[kKeepSpectra ? kB : 1][4];
+    // Pair and channel of the wave's first transform, advanced per tile.
+    const ChannelWalk walk(step * P::kFPB, channels);
+    ChannelPos pos = walk.at(tile * P::kFPB + wave * P::kFPW);
 
     for (; tile < tile_end; tile += step) {
         // Rows of this wave's transforms, as element offsets (-1: none).
@@ -99,7 +102,9 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
         for (int i = 0; i < kSteps; ++i) {
             const int e = 8 * lane + 512 * i;
             const long long tau = tile * P::kFPB + wave * P::kFPW + e / N;
-            const long long p = tau / channels, d = tau - p * channels;
+            long long p;
+            int d;
+            walk.locate(pos, e / N, p, d);
             const int k = e % N;
             base0[i] = tau < transforms ? (2 * p * channels + d) * N + k : -1;
             base1[i] = tau < transforms && 2 * p + 1 < batch ? ((2 * p + 1) * channels + d) * N + k
@@ -107,8 +112,11 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
         }
         // (past the last transform too: a channel is always a valid spectrum row)
 #pragma unroll
-        for (int f = 0; f < P::kFPW; ++f)
-            chan[f] = static_cast<int>((tile * P::kFPB + wave * P::kFPW + f) % channels);
+        for (int f = 0; f < P::kFPW; ++f) {
+            long long p;
+            walk.locate(pos, f, p, chan[f]);
+        }
+        pos = walk.advance(pos);
         u32x4 r0[kSteps], r1[kSteps];
 #pragma unroll
         for (int i = 0; i < kSteps; ++i) {
@@ -456,8 +464,11 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
     // count every tile of a workgroup has the same channel.
     long long spec_d = -1;
     cpx spec[4][4];
+    const ChannelWalk walk(step, channels);  // pair and channel of the tile, advanced per tile
+    ChannelPos pos = walk.at(tile);
     for (; tile < tile_end; tile += step) {
-        const long long p = tile / channels, d = tile - p * channels;
+        const long long p = pos.p, d = pos.d;
+        pos = walk.advance(pos);
         const long long row0 = (2 * p * channels + d) * N;
         const long long row1 = 2 * p + 1 < batch ? ((2 * p + 1) * channels + d) * N : -1;
         // ---- stage-1 inputs: values 64 w + 4 n + 1024 q + 256 e .. + 3 of both rows ----
