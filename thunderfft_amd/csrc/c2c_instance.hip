@@ -45,8 +45,10 @@ inline Grid make_grid(long long ntiles, int per_cu, int num_cus) {
 //     prefetch 95), 3 per CU 106, one tile per workgroup 122; 2 per CU with
 //     prefetch (224 VGPRs) 102 us.
 //   fp16 N = 64, 128 (VALU): one tile per workgroup.
-//   fp16 MFMA: 2 per CU, 87-94 us (two tiles per workgroup: 87-98 us; N = 4096
-//     with contiguous shares: 99 us), with prefetch except at N = 2048.
+//   fp16 MFMA: 2 per CU, 87-94 us, with prefetch except at N = 2048.  Runs
+//     of contiguous tiles per workgroup, which leave the balancing to the
+//     dispatcher, are slower: 2 tiles 87-98 us, 4-32 tiles 93-110 us (the
+//     grid-stride walk keeps all workgroups on neighbouring tiles).
 // `direct` (VALU kernel): tiles move between HBM and the first pass's
 // registers with no LDS staging (DirectIO, fft_tile.hpp).  fp32, same box:
 // N = 256 170 vs 175 us, 512 172 vs 174, 2048 180 vs 184, 4096 179 vs 183;
