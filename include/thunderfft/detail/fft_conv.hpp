@@ -73,9 +73,10 @@ conv1d_kernel(const IO* __restrict__ x, const IO* __restrict__ h, IO* __restrict
         io.load(nx, x, tile, batch);
         if constexpr (kPerSignal) io.load(nh, h, tile, batch);
     }
-    const long long total = (tile_end - tile + step - 1) / step;
-    for (; tile < tile_end; tile += step) {
-        progress_priority((tile_end - tile + step - 1) / step, total);
+    long long left = (tile_end - tile + step - 1) / step;  // tiles still to do, this one included
+    const ProgressPriority priority(left);
+    for (; tile < tile_end; tile += step, --left) {
+        priority.set(left);
         cpx v[16];
         if constexpr (kPrefetch) {
             typename T::Raw rx = nx, rh;
@@ -336,9 +337,10 @@ conv2d64_kernel(const IO* __restrict__ x, const IO* __restrict__ h, IO* __restri
 #pragma unroll
     for (int i = 0; i < 16; ++i) hs[i] = {hs[i].re * kScale, hs[i].im * kScale};
     __syncthreads();  // the filter's E2 reads are done before the first E1 writes
-    const long long total = (img_end - img + step - 1) / step;
-    for (; img < img_end; img += step) {
-        progress_priority((img_end - img + step - 1) / step, total);
+    long long left = (img_end - img + step - 1) / step;  // tiles still to do, this one included
+    const ProgressPriority priority(left);
+    for (; img < img_end; img += step, --left) {
+        priority.set(left);
         cpx v[16];
         conv2d::decode(raw, v);
         if (img + step < img_end) conv2d::load(raw, x, img + step, tid);

@@ -1115,9 +1115,10 @@ conv2d64_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ 
 #pragma unroll
         for (int t = 0; t < 4; ++t) hs[k][t] = {hs[k][t].re * (1.0f / 4096), hs[k][t].im * (1.0f / 4096)};
 
-    const long long total = (img_end - img + step - 1) / step;
-    for (; img < img_end; img += step) {
-        progress_priority((img_end - img + step - 1) / step, total);
+    long long left = (img_end - img + step - 1) / step;  // tiles still to do, this one included
+    const ProgressPriority priority(left);
+    for (; img < img_end; img += step, --left) {
+        priority.set(left);
         // A's previous readers (the filter's F1, or the last image's inverse
         // exchange reads) passed a barrier since; B's (F2 reads) pass the one
         // after this staging.

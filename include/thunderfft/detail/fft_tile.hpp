@@ -379,19 +379,27 @@ struct DirectIO {
 // end; with it a workgroup that gets ahead yields issue slots to those behind.
 // Measured for the VALU-bound fp32 convolutions (conv1d of 16384 signals of
 // 2048 with per-signal filters: 151 against 156-157 us; conv2d of 8192
-// images: 1.5%); the MFMA convolutions measured slower with it (real conv1d
-// N = 256: 61.5 against 58 us), so they do not use it.
-__device__ __forceinline__ void progress_priority(long long left, long long total) {
-    const long long level = total > 0 ? (4 * left - 1) / total : 3;
-    if (level >= 3)
-        __builtin_amdgcn_s_setprio(3);
-    else if (level == 2)
-        __builtin_amdgcn_s_setprio(2);
-    else if (level == 1)
-        __builtin_amdgcn_s_setprio(1);
-    else
-        __builtin_amdgcn_s_setprio(0);
-}
+// images: 1.5%) and the fp16 conv2d (67.8 against 66.7 us); the MFMA conv1d
+// kernels measured slower with it (real conv1d N = 256: 61.5 against 58 us),
+// so they do not use it.
+// The level is floor((4 left - 1) / total), decided by comparing `left`
+// with three thresholds computed once (left >= ceil((l total + 1) / 4) for
+// level >= l), so a walk pays no division per tile.
+struct ProgressPriority {
+    long long t1, t2, t3;
+    __device__ __forceinline__ explicit ProgressPriority(long long total)
+        : t1((total + 4) / 4), t2((2 * total + 4) / 4), t3((3 * total + 4) / 4) {}
+    __device__ __forceinline__ void set(long long left) const {
+        if (left >= t3)
+            __builtin_amdgcn_s_setprio(3);
+        else if (left >= t2)
+            __builtin_amdgcn_s_setprio(2);
+        else if (left >= t1)
+            __builtin_amdgcn_s_setprio(1);
+        else
+            __builtin_amdgcn_s_setprio(0);
+    }
+};
 
 // The tiles of workgroup blockIdx.x: first, first + step, ... while < end
 // (first >= end when it has none).
