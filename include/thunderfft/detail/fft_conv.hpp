@@ -792,9 +792,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kValidMinWa
     // The span of group gg (this wave's windows) as 16-byte vectors, zero past
     // the signal's end; for signals that start on a 16-byte boundary.
     constexpr int kLoads = kSpan / (64 * kVec);
-    auto span_load = [&](long long gg, W4 (&r)[kLoads]) {
-        const long long bb = gg / groups_per_signal;
-        const long long s0 = ((gg - bb * groups_per_signal) * P::kFPB + wave * kWindowsPerWave) * V;
+    // Signal and group within it of the walk's groups, advanced per step.
+    const DivWalk walk(step, groups_per_signal);
+    DivPos pos = walk.at(g);
+    auto span_load = [&](DivPos gp, W4 (&r)[kLoads]) {
+        const long long bb = gp.q;
+        const long long s0 = (gp.r * P::kFPB + wave * kWindowsPerWave) * V;
         const long long av = len - s0 < need ? len - s0 : need;
         const IO* sp = x + bb * len + s0;
 #pragma unroll
@@ -816,18 +819,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kValidMinWa
     // Prefetch only when every signal starts on a 16-byte boundary.
     const bool prefetch = kValidPrefetch<IO> && x16 && len % kVec == 0;
     W4 next[kLoads];
-    if (prefetch && g < g_end) span_load(g, next);
+    if (prefetch && g < g_end) span_load(pos, next);
     for (; g < g_end; g += step) {
-        const long long b = g / groups_per_signal;
+        const long long b = pos.q;
         // This wave's first window, and where its input span and its outputs
         // start in signal b (both w0 * V, a multiple of 16 values).
-        const long long w0 = (g - b * groups_per_signal) * P::kFPB + wave * kWindowsPerWave;
+        const long long w0 = pos.r * P::kFPB + wave * kWindowsPerWave;
         const long long span0 = w0 * V;
+        pos = walk.advance(pos);
         W4 cur[kLoads];
         if (prefetch) {
 #pragma unroll
             for (int i = 0; i < kLoads; ++i) cur[i] = next[i];
-            if (g + step < g_end) span_load(g + step, next);
+            if (g + step < g_end) span_load(pos, next);
         }
         if (span0 >= out_len) continue;  // no window of this wave has an output
         const long long avail = len - span0 < need ? len - span0 : need;  // > 0

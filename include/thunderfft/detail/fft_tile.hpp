@@ -422,4 +422,26 @@ __device__ __forceinline__ void tile_walk(long long ntiles, int tiles_per_block,
     }
 }
 
+// Quotient and remainder of a walk index g by d (g = q d + r), advanced by
+// the walk's constant step without a 64-bit division per step.
+struct DivPos {
+    long long q, r;
+};
+struct DivWalk {
+    long long d, adv_q, adv_r;
+    __device__ __forceinline__ DivWalk(long long step, long long divisor)
+        : d(divisor), adv_q(step / divisor), adv_r(step - (step / divisor) * divisor) {}
+    __device__ __forceinline__ DivPos at(long long g) const {
+        const long long q = g / d;
+        return {q, g - q * d};
+    }
+    // (adv_r < d and p.r < d: at most one carry)
+    __device__ __forceinline__ DivPos advance(DivPos p) const {
+        p.q += adv_q;
+        p.r += adv_r;
+        if (p.r >= d) p.r -= d, ++p.q;
+        return p;
+    }
+};
+
 }  // namespace thff
