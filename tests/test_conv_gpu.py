@@ -294,15 +294,18 @@ def test_conv2d_matches_direct_convolution(T):
         assert m["rel_l2"] <= GATE and m["rel_l2"] <= TIGHT[T], label
 
 
-def test_config5_conv2d_64x64():
-    """8192 float2 images of 64 x 64, shared 7 x 7-corner filter (the benchmarked conv2d)."""
+@pytest.mark.parametrize("T", ["float", "half"])
+def test_config5_conv2d_64x64(T):
+    """8192 images of 64 x 64, shared 7 x 7-corner filter (the benchmarked conv2d):
+    every workgroup walks several images (the next one's loads in flight)."""
     import torch
 
     import thunderfft_amd as thff
 
-    T, batch = "float", 8192
+    batch = 8192
     seed = oracle.BENCH_SEED_BASE + 4096
-    x = torch.empty(2 * 4096 * batch, dtype=torch.float32, device="cuda")
+    x = torch.empty(2 * 4096 * batch, dtype=torch.float32 if T == "float" else torch.float16,
+                    device="cuda")
     thff.fill_uniform(T, x, 4096 * batch, seed)
     y = torch.empty_like(x)
     thff.ThunderFFTInitialize(T, 64)
@@ -314,8 +317,9 @@ def test_config5_conv2d_64x64():
     sub = from_device(y.view(batch, 2 * 4096)[torch.from_numpy(rows).cuda()].contiguous(), T)
     xin = np.concatenate([oracle.uniform(4096, 1, seed, first_element=int(r) * 4096)
                           for r in rows]).reshape(len(rows), 64, 64)
-    m = oracle.metrics(sub.reshape(len(rows), 64, 64), oracle.circconv2d(xin, h))
-    print(f"conv2d 64x64 batch={batch} subset rel_l2={m['rel_l2']:.3e}", flush=True)
+    xin = oracle.represent(xin, T)
+    m = oracle.metrics(sub.reshape(len(rows), 64, 64), oracle.circconv2d(xin, oracle.represent(h, T)))
+    print(f"{T} conv2d 64x64 batch={batch} subset rel_l2={m['rel_l2']:.3e}", flush=True)
     assert m["nonfinite"] == 0 and m["rel_l2"] <= GATE and m["rel_l2"] <= TIGHT[T]
 
     # (2) every image: a unit impulse at (dr, dc) rolls every image by (dr, dc)
@@ -323,8 +327,8 @@ def test_config5_conv2d_64x64():
     imp = np.zeros((64, 64), dtype=np.complex64)
     imp[dr, dc] = 1
     thff.ThunderFFT_conv2d(T, 64, 64, x, to_device(imp, T), y, batch)
-    want = torch.roll(x.view(batch, 64, 64, 2), shifts=(dr, dc), dims=(1, 2))
-    err = float(torch.linalg.vector_norm(y.view(batch, 64, 64, 2) - want) /
+    want = torch.roll(x.view(batch, 64, 64, 2).float(), shifts=(dr, dc), dims=(1, 2))
+    err = float(torch.linalg.vector_norm(y.view(batch, 64, 64, 2).float() - want) /
                 torch.linalg.vector_norm(want))
     print(f"  impulse roll over all images rel_l2={err:.3e}", flush=True)
     assert np.isfinite(err) and err <= TIGHT[T]
