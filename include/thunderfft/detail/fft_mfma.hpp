@@ -847,3 +847,191 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
 }
 
 }  // namespace thff
+
+namespace thff {
+
+// ---------------------------------------------------------------------------
+// half2 C2C of N = 2048 = 8 x 256 on MFMA, two transforms per workgroup tile
+// (4 waves, 16 values per lane).  With n = t + 256 j (j < 8), t = t0 + 16 t1
+// and k = k1 + 8 k' (k1 < 8), k' = k2 + 16 k3:
+//   1. DFT8 over j of x[t + 256 j] -> Y1[t][k1], two 8-point DFTs per MFMA
+//      column (block-diagonal operands, dft8_pair_operands): wave w, lane
+//      (n, q), block b carries transform f = w / 2, sequence
+//      t = 128 (w & 1) + 64 (q / 2) + 4 n + b, inputs j = 4 (q & 1) + e -- one
+//      16-byte load per e straight from HBM, as in the N = 4096 kernel -- and
+//      receives outputs k1 = 2 q + i of its column's two sequences
+//      (y[2 H + i]: sequence t + 64 H of the column, t with q / 2 = 0).
+//   2. Y1 *= W_2048^(t k1); workgroup exchange into the N = 4096 kernel's
+//      stage-2 layout: matrix 8 f + k1 (wave 2 f + k1 / 4, block k1 % 4) holds
+//      the 256-point sequence over t of (f, k1).
+//   3-5. That kernel's stages 2 and 3 as a DFT256 over t = t0 + 16 t1: DFT16
+//      over t1, W_256^(t0 k2), wave-local transpose, DFT16 over t0 -> lane
+//      (n, q), block b of wave w: X_f[k1 + 8 k2 + 128 k3], k1 = 4 (w & 1) + b,
+//      k2 = n, k3 = q + 4 r; staged out in 16-byte chunks (out_chunk).
+// The exchange matrices sit 264 dwords apart, which keeps stage 1's writers
+// (matrices 2 q apart within an instruction) conflict-free; the readers are
+// the N = 4096 kernel's.
+struct Mfma2048 {
+    static constexpr int N = 2048;
+    static constexpr int kMatrix = 264;
+    static constexpr int kExchange = 16 * kMatrix;
+    static constexpr int kOut = 4096;  // two transforms
+    __device__ static __forceinline__ int xaddr(int m, int t0, int t1) {
+        return kMatrix * m + 16 * t0 + 4 * (((t1 >> 2) + (t0 >> 2)) & 3) + ((t1 + m) & 3);
+    }
+};
+
+// A-operand registers of two 8-point DFTs per column (block-diagonal real
+// 32 x 32 matrix): half H produces sequence H's outputs k1 = m / 2 (row m,
+// part m % 2) from inputs K = 16 H ... 16 H + 15 (input j = (K % 16) / 2,
+// part K % 2); entries of the other sequence's inputs are zero.
+template <bool FWD>
+__device__ __forceinline__ void dft8_pair_operands(f16x8 (&a)[2], int lane) {
+    const int m = lane & 15, kq = lane >> 4;
+    const int k1 = m >> 1, o = m & 1;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int kk = 8 * kq + e;
+            const int seq = kk >> 4, j = (kk & 15) >> 1, p = kk & 1;
+            const int ang = (2 * j * k1) & 15;  // W_8^(j k1) = W_16^(2 j k1)
+            const float c = kCos16[ang];
+            const float s = FWD ? -kSin16[ang] : kSin16[ang];
+            const float v = o == 0 ? (p == 0 ? c : -s) : (p == 0 ? s : c);
+            a[h][e] = static_cast<_Float16>(seq == h ? v : 0.0f);
+        }
+    }
+}
+
+template <bool FWD, bool kPrefetch>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void c2c_mfma2048_kernel(
+    const __half2* __restrict__ in, __half2* __restrict__ out, int batch,
+    const float2* __restrict__ tw, int tiles_per_block) {
+    using P = Mfma2048;
+    constexpr int N = P::N;
+    __shared__ __align__(16) unsigned xbuf[P::kExchange];
+    __shared__ __align__(16) unsigned obuf[P::kOut];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int n = lane & 15, q = lane >> 4;
+    const int f = wave >> 1;  // this wave's transform within the tile (stage 1)
+    unsigned* const region = xbuf + 4 * P::kMatrix * wave;
+
+    f16x8 a8[2], a[2];
+    dft8_pair_operands<FWD>(a8, lane);
+    dft16_operands<FWD>(a, lane);
+    // Twiddles: W_2048^(t k1), t = 128 (w & 1) + 64 H + 4 n + b, k1 = 2 q + i
+    // (r = 2 H + i); W_256^(t0 k2) = W_2048^(8 n k2), k2 = q + 4 r.
+    cpx w1[4][4], w2[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = 128 * (wave & 1) + 64 * (r >> 1) + 4 * n + b, k1 = 2 * q + (r & 1);
+            const float2 x = tw[(t * k1) & (N - 1)];
+            w1[b][r] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+        }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float2 x = tw[(8 * n * (q + 4 * r)) & (N - 1)];
+        w2[r] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+    }
+
+    const long long ntiles = (static_cast<long long>(batch) + 1) / 2;
+    long long tile, tile_end, step;
+    tile_walk(ntiles, tiles_per_block, tile, tile_end, step);
+    if (tile >= tile_end) return;  // uniform over the workgroup
+
+    // Inputs j = 4 (q & 1) + e of the lane's blocks b = 0..3:
+    // x_f[128 (w & 1) + 64 (q / 2) + 4 n + b + 256 j]; zero past the batch.
+    auto load = [&](u32x4 (&r)[4], long long tl) {
+        const bool ok = 2 * tl + f < batch;
+        const __half2* src = in + (2 * tl + f) * N + 128 * (wave & 1) + 64 * (q >> 1) + 4 * n +
+                             1024 * (q & 1);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            r[e] = ok ? ld_nt(reinterpret_cast<const u32x4*>(src + 256 * e)) : u32x4{};
+    };
+
+    u32x4 next[4];
+    if constexpr (kPrefetch) load(next, tile);
+    for (; tile < tile_end; tile += step) {
+        u32x4 cur[4];
+        if constexpr (kPrefetch) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cur[i] = next[i];
+            if (tile + step < tile_end) load(next, tile + step);
+        } else {
+            load(cur, tile);
+        }
+
+        // ---- stage 1: two DFT8s over j per column, then W_2048^(t k1) ----
+        cpx y[4][4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            u32x4 x;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = cur[e][b];
+            dft16_block(a8, as_f16x8(x), y[b]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) y[b][r] = cmul(y[b][r], w1[b][r]);
+        }
+        __syncthreads();  // every wave is done with the previous tile's exchange buffer
+        // ---- exchange: matrix 8 f + k1, t0 = t % 16, t1 = t / 16 ----
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                xbuf[P::xaddr(8 * f + 2 * q + (r & 1), 4 * (n & 3) + b,
+                              8 * (wave & 1) + 4 * (r >> 1) + (n >> 2))] = pack_half2(y[b][r]);
+        __syncthreads();
+        // ---- stage 2: block b holds matrix 4 w + b; lane (t0 = n, chunk q of t1) ----
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const u32x4 raw = *reinterpret_cast<const u32x4*>(
+                region + P::kMatrix * b + 16 * n + 4 * ((q + (n >> 2)) & 3));
+            u32x4 x;  // t1 = 4 q + e sits at position (e + m) & 3 = (e + b) & 3
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = raw[(e + b) & 3];
+            dft16_block(a, as_f16x8(x), y[b]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) y[b][r] = cmul(y[b][r], w2[r]);
+        }
+        // ---- wave-local transpose: row 16 b + k2 holds the 16 t0 of (k1, k2) ----
+        wave_lds_sync();
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int k2 = q + 4 * r;
+                region[(16 * b + k2) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] = pack_half2(y[b][r]);
+            }
+        wave_lds_sync();
+        // ---- stage 3: DFT16 over t0 -> X_f[k1 + 8 k2 + 128 k3], k2 = n, k3 = q + 4 r ----
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const u32x4 x = *reinterpret_cast<const u32x4*>(
+                region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+            dft16_block(a, as_f16x8(x), y[b]);
+        }
+        // ---- output: chunk K = (f' 2048 + 4 (w & 1) + 8 n + 128 k3) / 4 of the
+        // tile holds k1 = 4 (w & 1) + b, b = 0..3 (f' = w / 2) ----
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            reinterpret_cast<u32x4*>(obuf)[Mfma4096::out_chunk(512 * f + (wave & 1) + 2 * n +
+                                                               32 * (q + 4 * r))] =
+                u32x4{pack_half2(y[0][r]), pack_half2(y[1][r]), pack_half2(y[2][r]),
+                      pack_half2(y[3][r])};
+        __syncthreads();
+        __half2* dst = out + 2 * tile * N;
+        const bool second = 2 * tile + 1 < batch;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i < 2 || second)
+                st_nt(reinterpret_cast<u32x4*>(dst + 4 * tid + 1024 * i),
+                      reinterpret_cast<const u32x4*>(obuf)[Mfma4096::out_chunk(tid + 256 * i)]);
+    }
+}
+
+}  // namespace thff

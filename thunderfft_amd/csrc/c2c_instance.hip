@@ -41,11 +41,12 @@ inline Grid make_grid(long long ntiles, int per_cu, int num_cus) {
 //     per workgroup: 188-194 us); with direct movement, same box: 178 / 180 us
 //     against 12 per CU 181 / 179, 8 per CU 184 / 180, 4 per CU 189 / 181,
 //     8 per CU without prefetch 186 / 186, one tile per workgroup 181 / 186.
-//   fp16 N = 2048 (MFMA): 2 per CU 93-95 us against 1 per CU 111 (with
-//     prefetch 95), 3 per CU 106, one tile per workgroup 122; 2 per CU with
-//     prefetch (224 VGPRs) 102 us.
+//   fp16 N = 2048 (three-stage MFMA, two transforms per tile): 2 per CU with
+//     prefetch 88.2-88.5 us, against 90.6 at 3 per CU and 105.6 without
+//     prefetch (the two-stage one-transform-per-wave kernel it replaced:
+//     93-95 us at 2 per CU).
 //   fp16 N = 64, 128 (VALU): one tile per workgroup.
-//   fp16 MFMA: 2 per CU, 87-94 us, with prefetch except at N = 2048.  Runs
+//   fp16 MFMA: 2 per CU with prefetch, 86-91 us.  Runs
 //     of contiguous tiles per workgroup, which leave the balancing to the
 //     dispatcher, are slower: 2 tiles 87-98 us, 4-32 tiles 93-110 us (the
 //     grid-stride walk keeps all workgroups on neighbouring tiles).
@@ -66,15 +67,15 @@ constexpr LaunchShape launch_shape(int precision) {
         return N <= 1024 ? LaunchShape{0, false, N == 256 || N == 512}
                          : LaunchShape{16, true, true};
     if (N <= 128) return {0, false};
-    return {2, N != 2048};
+    return {2, true};
 }
 
 // half2 lengths whose radix-16 stages run on MFMA (fft_mfma.hpp): N = 256*C
-// (two stages) and N = 4096 (three stages).
+// (two stages) and N = 2048, 4096 (three stages across a workgroup).
 template <int N>
-inline constexpr bool kHalfOnMfma = N >= 256 && N <= 2048;
+inline constexpr bool kHalfOnMfma = N >= 256 && N <= 1024;
 template <int N>
-inline constexpr bool kHalfOnMfma3 = N == 4096;
+inline constexpr bool kHalfOnMfma3 = N == 2048 || N == 4096;
 
 // Only the launch shape in use is instantiated.
 template <class IO, int N, bool FWD>
@@ -92,12 +93,16 @@ void enqueue_mfma(Grid g, const __half2* x, __half2* y, int batch, const float2*
                                                                      g.tiles_per_block);
 }
 
-template <bool FWD>
-void enqueue_mfma4096(Grid g, const __half2* x, __half2* y, int batch, const float2* tw,
-                      hipStream_t stream) {
-    constexpr bool kPf = launch_shape<4096>(1).prefetch;
-    c2c_mfma4096_kernel<FWD, kPf><<<g.blocks, 256, 0, stream>>>(x, y, batch, tw,
-                                                                g.tiles_per_block);
+template <int N, bool FWD>
+void enqueue_mfma3(Grid g, const __half2* x, __half2* y, int batch, const float2* tw,
+                   hipStream_t stream) {
+    constexpr bool kPf = launch_shape<N>(1).prefetch;
+    if constexpr (N == 2048)
+        c2c_mfma2048_kernel<FWD, kPf><<<g.blocks, 256, 0, stream>>>(x, y, batch, tw,
+                                                                    g.tiles_per_block);
+    else
+        c2c_mfma4096_kernel<FWD, kPf><<<g.blocks, 256, 0, stream>>>(x, y, batch, tw,
+                                                                    g.tiles_per_block);
 }
 
 // Buffers that are element-aligned but not 16-byte aligned (any vec2_t<T>
@@ -129,7 +134,7 @@ hipError_t launch_c2c(int precision, bool forward, bool aligned16, const void* i
         return hipGetLastError();
     }
     const bool mfma = precision != 0 && kHalfOnMfma<N>;
-    long long fpb = C2CPlan<N>::kFPB;  // 1 for N = 4096 on either kernel
+    long long fpb = C2CPlan<N>::kFPB;  // 2 for N = 2048 and 1 for N = 4096 on either kernel
     if constexpr (kHalfOnMfma<N>)
         if (mfma) fpb = MfmaPlan<N / 256>::kFPB;
     const long long ntiles = (static_cast<long long>(batch) + fpb - 1) / fpb;
@@ -151,9 +156,9 @@ hipError_t launch_c2c(int precision, bool forward, bool aligned16, const void* i
                 enqueue_mfma<N, false>(g, x, y, batch, tw, stream);
         } else if constexpr (kHalfOnMfma3<N>) {
             if (forward)
-                enqueue_mfma4096<true>(g, x, y, batch, tw, stream);
+                enqueue_mfma3<N, true>(g, x, y, batch, tw, stream);
             else
-                enqueue_mfma4096<false>(g, x, y, batch, tw, stream);
+                enqueue_mfma3<N, false>(g, x, y, batch, tw, stream);
         } else if (forward) {
             enqueue<__half2, N, true>(g, x, y, batch, tw, stream);
         } else {
