@@ -1035,3 +1035,144 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void c
 }
 
 }  // namespace thff
+
+namespace thff {
+
+// ---------------------------------------------------------------------------
+// half2 C2C of N = 128 = 16 x 8 on MFMA, eight transforms per wave (16 values
+// per lane), a tile of four waves.  With n = t + 8 j (t < 8, j < 16) and
+// k = k1 + 16 k2 (k2 < 8):
+//   1. DFT16 over j of x_f[t + 8 j] from the wave's staged values: block b,
+//      column n holds transform f = 2 b + n / 8 of the wave, sequence
+//      t = n % 8 -> lane (n, q) receives k1 = q + 4 r;
+//   2. Y1 *= W_128^(t k1);
+//   3. wave-local transpose: block b, column k1 holds transforms 2 b and
+//      2 b + 1 (lane groups q / 2), inputs t = 4 (q % 2) + e;
+//   4. two DFT8s over t per column (dft8_pair_operands) -> lane (n, q),
+//      block b: y[b][2 H + i] = X_f[n + 16 (2 q + i)], f = 2 b + H;
+//   5. staged out in 16-byte pieces.
+// LDS per wave: input staging padded k + 8 (k / 32) (the stride-8 stage-1
+// reads of the 64 lanes hit 64 banks), the transpose with 16-byte chunks
+// rotated by column / 4, output staging padded k + 16 (k / 64) (dword writes
+// and 16-byte reads conflict-free).
+struct Mfma128 {
+    static constexpr int N = 128;
+    static constexpr int kFPW = 8;          // transforms per wave
+    static constexpr int kFPB = 4 * kFPW;   // per tile
+    static constexpr int kWaveVals = kFPW * N;
+    static constexpr int kRegion = 1272;    // in_pad(1023) + 1 dwords
+    __device__ static __forceinline__ int in_pad(int k) { return k + 8 * (k >> 5); }
+    __device__ static __forceinline__ int out_pad(int k) { return k + 16 * (k >> 6); }
+    __device__ static __forceinline__ int taddr(int b, int col, int qq, int e) {
+        return 256 * b + 16 * col + 4 * ((qq + (col >> 2)) & 3) + e;
+    }
+};
+
+template <bool FWD, bool kPrefetch>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void c2c_mfma128_kernel(
+    const __half2* __restrict__ in, __half2* __restrict__ out, int batch,
+    const float2* __restrict__ tw, int tiles_per_block) {
+    using P = Mfma128;
+    constexpr int N = P::N;
+    __shared__ __align__(16) unsigned lds[4 * P::kRegion];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int n = lane & 15, q = lane >> 4;
+    unsigned* const region = lds + wave * P::kRegion;
+
+    f16x8 a[2], a8[2];
+    dft16_operands<FWD>(a, lane);
+    dft8_pair_operands<FWD>(a8, lane);
+    cpx w1[4];  // W_128^(t k1), t = n % 8, k1 = q + 4 r
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float2 x = tw[((n & 7) * (q + 4 * r)) & (N - 1)];
+        w1[r] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
+    }
+
+    const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
+    long long tile, tile_end, step;
+    tile_walk(ntiles, tiles_per_block, tile, tile_end, step);
+    if (tile >= tile_end) return;  // uniform over the workgroup
+
+    // Valid values (0..kWaveVals) of this wave's transforms in tile tl.
+    auto valid = [&](long long tl) {
+        const long long v = (static_cast<long long>(batch) - tl * P::kFPB - wave * P::kFPW) * N;
+        return v <= 0 ? 0 : (v >= P::kWaveVals ? P::kWaveVals : static_cast<int>(v));
+    };
+    auto load = [&](u32x4 (&r)[4], long long tl) {
+        const int nv = valid(tl);
+        const __half2* src = in + (tl * P::kFPB + wave * P::kFPW) * N;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * lane + 256 * i;
+            r[i] = e < nv ? ld_nt(reinterpret_cast<const u32x4*>(src + e)) : u32x4{};
+        }
+    };
+
+    u32x4 next[4];
+    if constexpr (kPrefetch) load(next, tile);
+    for (; tile < tile_end; tile += step) {
+        u32x4 cur[4];
+        if constexpr (kPrefetch) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cur[i] = next[i];
+            if (tile + step < tile_end) load(next, tile + step);
+        } else {
+            load(cur, tile);
+        }
+        wave_lds_sync();  // the previous tile's output reads are done
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<u32x4*>(region + P::in_pad(4 * lane + 256 * i)) = cur[i];
+        wave_lds_sync();
+
+        // ---- stage 1: DFT16 over j, then W_128^(t k1) ----
+        cpx y[4][4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int base = 128 * (2 * b + (n >> 3)) + (n & 7);
+            u32x4 x;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = region[P::in_pad(base + 8 * (4 * q + e))];
+            dft16_block(a, as_f16x8(x), y[b]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) y[b][r] = cmul(y[b][r], w1[r]);
+        }
+        // ---- transpose: (f, t, k1) -> block f / 2, column k1, group 2 (f % 2) + t / 4 ----
+        wave_lds_sync();
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                region[P::taddr(b, q + 4 * r, 2 * (n >> 3) + ((n & 7) >> 2), n & 3)] =
+                    pack_half2(y[b][r]);
+        wave_lds_sync();
+        // ---- stage 2: two DFT8s over t per column ----
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const u32x4 x = *reinterpret_cast<const u32x4*>(region + P::taddr(b, n, q, 0));
+            dft16_block(a8, as_f16x8(x), y[b]);
+        }
+        // ---- output staging: X_f[n + 16 (2 q + i)], f = 2 b + H ----
+        wave_lds_sync();
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                region[P::out_pad(128 * (2 * b + (r >> 1)) + n + 16 * (2 * q + (r & 1)))] =
+                    pack_half2(y[b][r]);
+        wave_lds_sync();
+        const int nv = valid(tile);
+        __half2* dst = out + (tile * P::kFPB + wave * P::kFPW) * N;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * lane + 256 * i;
+            if (e < nv)
+                st_nt(reinterpret_cast<u32x4*>(dst + e),
+                      *reinterpret_cast<const u32x4*>(region + P::out_pad(e)));
+        }
+    }
+}
+
+}  // namespace thff

@@ -45,7 +45,10 @@ inline Grid make_grid(long long ntiles, int per_cu, int num_cus) {
 //     prefetch 88.2-88.5 us, against 90.6 at 3 per CU and 105.6 without
 //     prefetch (the two-stage one-transform-per-wave kernel it replaced:
 //     93-95 us at 2 per CU).
-//   fp16 N = 64, 128 (VALU): one tile per workgroup.
+//   fp16 N = 64 (VALU): one tile per workgroup.
+//   fp16 N = 128 (MFMA, c2c_mfma128_kernel): 2 per CU with prefetch 87.3 us,
+//     against 90.0 at 3 per CU, 99.5 with one tile per workgroup and 90.3-91.1
+//     for the VALU kernel (one tile per workgroup; device grids 93).
 //   fp16 MFMA: 2 per CU with prefetch, 86-91 us.  Runs
 //     of contiguous tiles per workgroup, which leave the balancing to the
 //     dispatcher, are slower: 2 tiles 87-98 us, 4-32 tiles 93-110 us (the
@@ -66,16 +69,20 @@ constexpr LaunchShape launch_shape(int precision) {
     if (precision == 0)
         return N <= 1024 ? LaunchShape{0, false, N == 256 || N == 512}
                          : LaunchShape{16, true, true};
+    if (N == 128) return {2, true};
     if (N <= 128) return {0, false};
     return {2, true};
 }
 
 // half2 lengths whose radix-16 stages run on MFMA (fft_mfma.hpp): N = 256*C
-// (two stages) and N = 2048, 4096 (three stages across a workgroup).
+// (two stages), N = 2048, 4096 (three stages across a workgroup) and N = 128
+// (a DFT16 and a DFT8 pair within a wave).
 template <int N>
 inline constexpr bool kHalfOnMfma = N >= 256 && N <= 1024;
 template <int N>
 inline constexpr bool kHalfOnMfma3 = N == 2048 || N == 4096;
+template <int N>
+inline constexpr bool kHalfOnMfma128 = N == 128;
 
 // Only the launch shape in use is instantiated.
 template <class IO, int N, bool FWD>
@@ -91,6 +98,13 @@ void enqueue_mfma(Grid g, const __half2* x, __half2* y, int batch, const float2*
     constexpr bool kPf = launch_shape<N>(1).prefetch;
     c2c_mfma_kernel<N / 256, FWD, kPf><<<g.blocks, 256, 0, stream>>>(x, y, batch, tw,
                                                                      g.tiles_per_block);
+}
+
+template <bool FWD>
+void enqueue_mfma128(Grid g, const __half2* x, __half2* y, int batch, const float2* tw,
+                     hipStream_t stream) {
+    constexpr bool kPf = launch_shape<128>(1).prefetch;
+    c2c_mfma128_kernel<FWD, kPf><<<g.blocks, 256, 0, stream>>>(x, y, batch, tw, g.tiles_per_block);
 }
 
 template <int N, bool FWD>
@@ -159,6 +173,11 @@ hipError_t launch_c2c(int precision, bool forward, bool aligned16, const void* i
                 enqueue_mfma3<N, true>(g, x, y, batch, tw, stream);
             else
                 enqueue_mfma3<N, false>(g, x, y, batch, tw, stream);
+        } else if constexpr (kHalfOnMfma128<N>) {
+            if (forward)
+                enqueue_mfma128<true>(g, x, y, batch, tw, stream);
+            else
+                enqueue_mfma128<false>(g, x, y, batch, tw, stream);
         } else if (forward) {
             enqueue<__half2, N, true>(g, x, y, batch, tw, stream);
         } else {
