@@ -884,8 +884,12 @@ struct Mfma2048 {
 // A-operand registers of two 8-point DFTs per column (block-diagonal real
 // 32 x 32 matrix): half H produces sequence H's outputs k1 = m / 2 (row m,
 // part m % 2) from inputs K = 16 H ... 16 H + 15 (input j = (K % 16) / 2,
-// part K % 2); entries of the other sequence's inputs are zero.
-template <bool FWD>
+// part K % 2); entries of the other sequence's inputs are zero.  With
+// kPermuted the columns follow the device API's N = 2048 fragment order
+// instead: lane group kq of the data operand holds sequence kq % 2's inputs
+// j = 2 c + kq / 2 in its complex slots c = 0..3.  kArith computes the
+// entries with cis_rev instead of reading the constant table.
+template <bool FWD, bool kPermuted = false, bool kArith = false>
 __device__ __forceinline__ void dft8_pair_operands(f16x8 (&a)[2], int lane) {
     const int m = lane & 15, kq = lane >> 4;
     const int k1 = m >> 1, o = m & 1;
@@ -893,11 +897,19 @@ __device__ __forceinline__ void dft8_pair_operands(f16x8 (&a)[2], int lane) {
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const int kk = 8 * kq + e;
-            const int seq = kk >> 4, j = (kk & 15) >> 1, p = kk & 1;
+            const int slot = e >> 1, p = e & 1;
+            const int seq = kPermuted ? (kq & 1) : kq >> 1;
+            const int j = kPermuted ? 2 * slot + (kq >> 1) : 4 * (kq & 1) + slot;
             const int ang = (2 * j * k1) & 15;  // W_8^(j k1) = W_16^(2 j k1)
-            const float c = kCos16[ang];
-            const float s = FWD ? -kSin16[ang] : kSin16[ang];
+            float c, s;
+            if constexpr (kArith) {
+                const cpx cs = cis_rev(ang, 16);
+                c = cs.re;
+                s = FWD ? -cs.im : cs.im;
+            } else {
+                c = kCos16[ang];
+                s = FWD ? -kSin16[ang] : kSin16[ang];
+            }
             const float v = o == 0 ? (p == 0 ? c : -s) : (p == 0 ? s : c);
             a[h][e] = static_cast<_Float16>(seq == h ? v : 0.0f);
         }
@@ -1032,6 +1044,124 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void c
                 st_nt(reinterpret_cast<u32x4*>(dst + 4 * tid + 1024 * i),
                       reinterpret_cast<const u32x4*>(obuf)[Mfma4096::out_chunk(tid + 256 * i)]);
     }
+}
+
+// Per-lane coefficients of one direction of mfma2048_fft_regs: the
+// column-permuted DFT8-pair operands, the plain DFT16 operands, the stage-1
+// -> 2 twiddles W_2048^(t k1) (t = 4 (w & 1) + b + 8 n + 128 (r / 2),
+// k1 = 2 q + r % 2) and the stage-2 -> 3 twiddles W_2048^(8 n (q + 4 r)),
+// conjugated for the forward direction (tid: the lane's index in the
+// 256-lane block).  load() from the table, build() with cis_rev.
+struct Mfma2048Coeffs {
+    static constexpr int N = 2048;
+    f16x8 a8[2], a[2];
+    cpx w1[4][4], w2[4];
+
+    template <bool FWD, class Tw>
+    __device__ __forceinline__ void fill(int tid, Tw tw_at) {
+        const int wave = tid >> 6, lane = tid & 63, n = lane & 15, q = lane >> 4;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 4 * (wave & 1) + b + 8 * n + 128 * (r >> 1);
+                const cpx x = tw_at(t * (2 * q + (r & 1)));
+                w1[b][r] = FWD ? cpx{x.re, -x.im} : x;
+            }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const cpx x = tw_at(8 * n * (q + 4 * r));
+            w2[r] = FWD ? cpx{x.re, -x.im} : x;
+        }
+    }
+    template <bool FWD>
+    __device__ __forceinline__ void load(const float2* __restrict__ tw, int tid) {
+        dft8_pair_operands<FWD, true>(a8, tid & 63);
+        dft16_operands<FWD>(a, tid & 63);
+        fill<FWD>(tid, [&](int k) {
+            const float2 x = tw[k & (N - 1)];
+            return cpx{x.x, x.y};
+        });
+    }
+    template <bool FWD>
+    __device__ __forceinline__ void build(int tid) {
+        dft8_pair_operands<FWD, true, true>(a8, tid & 63);
+        dft16_operands_arith<FWD>(a, tid & 63);
+        fill<FWD>(tid, [](int k) { return cis_rev(k, N); });
+    }
+};
+
+// Two N = 2048 transforms per workgroup from registers, either direction,
+// for callers without the kernel's set-up (the device-side API).  Lane
+// (n, q) of wave w holds, in v[b][r], element 4 (w & 1) + b + 8 n +
+// 128 (q + 4 r) of transform w / 2 on entry and on return (the layout
+// c2c_mfma2048_kernel's three stages leave, so transforms chain).  In that
+// order block b's column n carries the sequences t = 4 (w & 1) + b + 8 n +
+// 128 H (H = q % 2) with inputs j = 2 r + q / 2, so stage 1 takes the
+// column-permuted DFT8-pair operands and leaves outputs k1 = 2 q + r % 2 of
+// sequence H = r / 2; W_2048^(t k1); the exchange into the kernel's stage-2
+// layout (t0 = t % 16 = 4 (w & 1) + b + 8 (n & 1), t1 = t / 16 = n / 2 + 8 H;
+// stride 264 keeps these writes conflict-free too); the kernel's stages 2
+// and 3.  xbuf: Mfma2048::kExchange dwords of LDS; two workgroup barriers,
+// the first before xbuf is written.  `k` holds this direction's coefficients.
+template <bool FWD>
+__device__ __forceinline__ void mfma2048_fft_regs(unsigned* xbuf, const Mfma2048Coeffs& k, int tid,
+                                                  cpx (&v)[4][4]) {
+    using P = Mfma2048;
+    const int wave = tid >> 6, lane = tid & 63, n = lane & 15, q = lane >> 4;
+    const int f = wave >> 1;
+    unsigned* const region = xbuf + 4 * P::kMatrix * wave;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        u32x4 xv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xv[r] = pack_half2(v[b][r]);
+        dft16_block(k.a8, as_f16x8(xv), v[b]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], k.w1[b][r]);
+    }
+    __syncthreads();  // every wave is done with xbuf
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            xbuf[P::xaddr(8 * f + 2 * q + (r & 1), 4 * (wave & 1) + b + 8 * (n & 1),
+                          (n >> 1) + 8 * (r >> 1))] = pack_half2(v[b][r]);
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const u32x4 raw = *reinterpret_cast<const u32x4*>(
+            region + P::kMatrix * b + 16 * n + 4 * ((q + (n >> 2)) & 3));
+        u32x4 xv;  // t1 = 4 q + e sits at position (e + m) & 3 = (e + b) & 3
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[e] = raw[(e + b) & 3];
+        dft16_block(k.a, as_f16x8(xv), v[b]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], k.w2[r]);
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            region[(16 * b + q + 4 * r) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] = pack_half2(v[b][r]);
+    wave_lds_sync();
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(
+            region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+        dft16_block(k.a, as_f16x8(xv), v[b]);
+    }
+}
+
+// As above, the coefficients read from the positive-angle table `tw` of
+// length 2048 for this call.
+template <bool FWD>
+__device__ __forceinline__ void mfma2048_fft_regs(unsigned* xbuf, const float2* __restrict__ tw,
+                                                  int tid, cpx (&v)[4][4]) {
+    Mfma2048Coeffs k;
+    k.template load<FWD>(tw, tid);
+    mfma2048_fft_regs<FWD>(xbuf, k, tid, v);
 }
 
 }  // namespace thff

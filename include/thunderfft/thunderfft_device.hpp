@@ -13,13 +13,14 @@
 //    length N.  Every lane holds 16 complex values ("the fragment").
 //  * Fragment order: register j of lane tid holds element
 //    fragment_element<T, N>(tid, j) of transform fragment_transform<T, N>(tid, j)
-//    of the block.  For float, and for half at N = 64, 128, 2048 (VALU
+//    of the block.  For float, and for half at N = 64, 128 (VALU
 //    transforms): transform tid / (N/16), element t + (N/16)*j,
-//    t = tid % (N/16).  For half at N = 256, 512, 1024, 4096 the transform
+//    t = tid % (N/16).  For half at N = 256 ... 4096 the transform
 //    runs on the matrix cores (v_mfma_f32_16x16x32_f16, as the library's own
 //    kernels) and the fragment is the MFMA layout: wave w = tid/64, lane
 //    n + 16q, j = 4b + r; N = 256C (C = 1, 2, 4): transform w*(4/C) + b/C,
-//    element n + 16*(b%C) + 16C*(q+4r); N = 4096: element
+//    element n + 16*(b%C) + 16C*(q+4r); N = 2048: transform w/2, element
+//    4*(w%2) + b + 8n + 128*(q+4r); N = 4096: element
 //    4w + b + 16n + 256*(q+4r).  Either way the same order holds before and after
 //    ThunderFFT_kernel_reg, in both directions, so a forward transform, a
 //    pointwise product and an inverse transform chain in registers with no
@@ -27,7 +28,8 @@
 //    the movement helpers below follow the order.
 //  * The workspace is caller-owned LDS of workspace_bytes<N, batch> bytes
 //    (8 bytes per complex value for both storage types: the FFT computes in
-//    fp32), 8-byte aligned.  All helpers are collective over the block, do
+//    fp32), 16-byte aligned (the MFMA transforms move 16-byte chunks through
+//    it; __shared__ __align__(16)).  All helpers are collective over the block, do
 //    no bounds checks and insert no barrier before their first access:
 //    __syncthreads() between a producer and a consumer of the same LDS, as
 //    in the reference.
@@ -102,10 +104,10 @@ struct layout_t {
 // reg2smem through it read and write every LDS bank once per instruction.
 // VALU order: one pad value per 16 (as pad_h); MFMA order (C = N/256): 16 pad
 // values after every 16C, so the four lane groups q (16C apart) land on
-// different banks.
+// different banks; N = 2048 and 4096: one pad value per 64.
 template <typename T, int N>
 using fragment_layout = std::conditional_t<
-    std::is_same_v<T, half> && N == 4096,
+    std::is_same_v<T, half> && (N == 2048 || N == 4096),
     layout_t<N, batch_per_block<N>, 1, N, 64, 1, false>,
     std::conditional_t<
     std::is_same_v<T, half> && (N == 512 || N == 1024),
@@ -122,7 +124,7 @@ using lane_twiddles = thff::LaneTwiddles<N>;
 // True where half fragments use the MFMA layout (see the contract above).
 template <typename T, int N>
 inline constexpr bool fragment_on_mfma =
-    std::is_same_v<T, half> && (N == 256 || N == 512 || N == 1024 || N == 4096);
+    std::is_same_v<T, half> && (N == 256 || N == 512 || N == 1024 || N == 2048 || N == 4096);
 
 // Transform (of the block's batch_per_block<N>) and element index held by
 // register j of lane tid.
@@ -130,6 +132,8 @@ template <typename T, int N>
 __device__ __forceinline__ int fragment_transform(int tid, int j) {
     if constexpr (fragment_on_mfma<T, N> && N == 4096) {
         return 0;
+    } else if constexpr (fragment_on_mfma<T, N> && N == 2048) {
+        return tid >> 7;
     } else if constexpr (fragment_on_mfma<T, N>) {
         constexpr int C = N / 256;
         return (tid >> 6) * (4 / C) + (j >> 2) / C;
@@ -142,6 +146,9 @@ __device__ __forceinline__ int fragment_element(int tid, int j) {
     if constexpr (fragment_on_mfma<T, N> && N == 4096) {
         const int lane = tid & 63;
         return 4 * (tid >> 6) + (j >> 2) + 16 * (lane & 15) + 256 * ((lane >> 4) + 4 * (j & 3));
+    } else if constexpr (fragment_on_mfma<T, N> && N == 2048) {
+        const int lane = tid & 63;
+        return 4 * ((tid >> 6) & 1) + (j >> 2) + 8 * (lane & 15) + 128 * ((lane >> 4) + 4 * (j & 3));
     } else if constexpr (fragment_on_mfma<T, N>) {
         constexpr int C = N / 256;
         const int lane = tid & 63;
@@ -210,6 +217,16 @@ __device__ __forceinline__ void ThunderFFT_kernel_reg(vec2_t<T>* __restrict__ re
         thff::mfma4096_fft_regs<forward>(static_cast<unsigned*>(workspace), W.table, tid, y);
 #pragma unroll
         for (int j = 0; j < 16; ++j) reg[j] = detail::from_cpx<T>(y[j >> 2][j & 3]);
+    } else if constexpr (fragment_on_mfma<T, N> && N == 2048) {
+        // The three-stage MFMA transform of the library's N = 2048 kernel
+        // (thff::mfma2048_fft_regs), both transforms of the block at once;
+        // 16.5 KiB of the workspace; two workgroup barriers.
+        thff::cpx y[4][4];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) y[j >> 2][j & 3] = detail::to_cpx<T>(reg[j]);
+        thff::mfma2048_fft_regs<forward>(static_cast<unsigned*>(workspace), W.table, tid, y);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) reg[j] = detail::from_cpx<T>(y[j >> 2][j & 3]);
     } else if constexpr (fragment_on_mfma<T, N>) {
         // The library's MFMA transform (thff::mfma_fft_regs): f16 data into
         // each DFT16 stage, fp32 accumulation and twiddles; wave w uses 4 KiB
@@ -247,13 +264,14 @@ __device__ __forceinline__ void ThunderFFT_kernel_reg(vec2_t<T>* __restrict__ re
 namespace detail {
 
 // The per-lane coefficients of the fp16 transform of length N: the MFMA
-// transforms' operands and twiddles (N = 256, 512, 1024, 4096) or the VALU
-// passes' twiddle factors (N = 64, 128, 2048).
+// transforms' operands and twiddles (N = 256 ... 4096) or the VALU passes'
+// twiddle factors (N = 64, 128).
 template <int N>
 using half_coefficients = std::conditional_t<
     N == 4096, thff::Mfma4096Coeffs,
+    std::conditional_t<N == 2048, thff::Mfma2048Coeffs,
     std::conditional_t<fragment_on_mfma<half, N>, thff::MfmaCoeffs<(N >= 256 ? N / 256 : 1)>,
-                       thff::LaneTwiddles<N>>>;
+                       thff::LaneTwiddles<N>>>>;
 
 }  // namespace detail
 
@@ -289,7 +307,7 @@ __device__ __forceinline__ void make_reg_b_precompute(Coeffs&& W_arg) {
     detail::check_shape<N, batch_per_block<N>>();
     const int tid = detail::block_tid();
     detail::half_coefficients<N> k;
-    if constexpr (N == 4096)
+    if constexpr (N == 2048 || N == 4096)
         k.template build<forward>(tid);
     else if constexpr (fragment_on_mfma<half, N>)
         k.template build<forward>(tid & 63);
@@ -320,6 +338,13 @@ __device__ __forceinline__ void ThunderFFT_kernel_reg(vec2_t<T>* __restrict__ re
 #pragma unroll
             for (int j = 0; j < 16; ++j) y[j >> 2][j & 3] = detail::to_cpx<T>(reg[j]);
             thff::mfma4096_fft_regs<forward>(static_cast<unsigned*>(workspace), k, tid, y);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) reg[j] = detail::from_cpx<T>(y[j >> 2][j & 3]);
+        } else if constexpr (N == 2048) {
+            thff::cpx y[4][4];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) y[j >> 2][j & 3] = detail::to_cpx<T>(reg[j]);
+            thff::mfma2048_fft_regs<forward>(static_cast<unsigned*>(workspace), k, tid, y);
 #pragma unroll
             for (int j = 0; j < 16; ++j) reg[j] = detail::from_cpx<T>(y[j >> 2][j & 3]);
         } else if constexpr (fragment_on_mfma<T, N>) {

@@ -104,7 +104,7 @@ def test_device_api_fft(ex, T, n):
 
 
 @pytest.mark.parametrize("T", ["float", "half"])
-@pytest.mark.parametrize("n", [64, 1024, 4096])
+@pytest.mark.parametrize("n", [64, 1024, 2048, 4096])
 def test_device_api_fused_filter(ex, T, n):
     import thunderfft_amd as thff
 
@@ -167,7 +167,7 @@ def test_device_api_precomputed_coefficients(ex, T, n):
 def test_fragment_order_is_a_bijection(ex, T):
     """fragment_transform / fragment_element map the block's 256 lanes x 16
     registers one-to-one onto its batch_per_block<N> transforms x N elements, for
-    every length (half at N = 256, 512, 1024, 4096 uses the MFMA layouts)."""
+    every length (half at N = 256 ... 4096 uses the MFMA layouts)."""
     import torch
 
     import thunderfft_amd as thff
@@ -181,3 +181,33 @@ def test_fragment_order_is_a_bijection(ex, T):
         assert m[:, 1].min() >= 0 and m[:, 1].max() < n, (T, n)
         flat = m[:, 0].astype(np.int64) * n + m[:, 1]
         assert np.unique(flat).size == bpb * n == 4096, (T, n)
+
+
+def documented_order(T, n, tid, j):
+    """The fragment order the device header's contract states: (transform,
+    element) of register j of lane tid."""
+    w, lane = tid // 64, tid % 64
+    nn, q, b, r = lane % 16, lane // 16, j // 4, j % 4
+    if T == "float" or n <= 128:
+        return tid // (n // 16), tid % (n // 16) + (n // 16) * j
+    if n == 2048:
+        return w // 2, 4 * (w % 2) + b + 8 * nn + 128 * (q + 4 * r)
+    if n == 4096:
+        return 0, 4 * w + b + 16 * nn + 256 * (q + 4 * r)
+    c = n // 256
+    return w * (4 // c) + b // c, nn + 16 * (b % c) + 16 * c * (q + 4 * r)
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+def test_fragment_order_matches_contract(ex, T):
+    """The order the kernels use is the one the header documents, so a caller
+    can index per-bin data (a filter spectrum) without calling the device
+    helpers."""
+    import torch
+
+    for n in SIZES:
+        d_map = torch.full((2 * 256 * 16,), -1, dtype=torch.int32, device="cuda")
+        assert ex.thffx_fragment_map(PREC[T], n, d_map.data_ptr(), None) == 0
+        m = d_map.cpu().numpy().reshape(256, 16, 2)
+        want = np.array([[documented_order(T, n, tid, j) for j in range(16)] for tid in range(256)])
+        assert np.array_equal(m, want), (T, n)
