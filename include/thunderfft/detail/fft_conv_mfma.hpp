@@ -94,7 +94,13 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
     const ChannelWalk walk(step * P::kFPB, channels);
     ChannelPos pos = walk.at(tile * P::kFPB + wave * P::kFPW);
 
-    for (; tile < tile_end; tile += step) {
+    // At N = 2048 (one transform per wave) a wave's issue priority falls as
+    // its workgroup gets ahead of the others: 70 against 72-73 us at 2^26
+    // samples; neutral at N <= 1024.
+    long long left = (tile_end - tile + step - 1) / step;
+    const ProgressPriority priority(left);
+    for (; tile < tile_end; tile += step, --left) {
+        if constexpr (C == 8) priority.set(left);
         // Rows of this wave's transforms, as element offsets (-1: none).
         long long base0[kSteps], base1[kSteps];
         int chan[P::kFPW];
@@ -307,7 +313,13 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
     u32x4 rn[kRaw];
     if constexpr (kPrefetchShared)
         if (tile < tile_end) load(x + offset(tile), valid(tile), rn);
-    for (; tile < tile_end; tile += step) {
+    // At N = 2048 a wave's issue priority falls as its workgroup gets ahead
+    // (ProgressPriority): 63.5 against 66-67 us (shared filter) and 91.0
+    // against 91.7-92.0 us (per-signal) at 2^25 values; neutral at N <= 1024.
+    long long left = (tile_end - tile + step - 1) / step;
+    const ProgressPriority priority(left);
+    for (; tile < tile_end; tile += step, --left) {
+        if constexpr (C == 8) priority.set(left);
         const int nv = valid(tile);
         const long long off = offset(tile);
         cpx v[kB][4];
@@ -727,7 +739,13 @@ conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict_
         keep(v);
         load(x + tile * N, zx);
     }
-    for (; tile < tile_end; tile += step) {
+    // A wave's issue priority falls as its workgroup gets ahead of the others
+    // (ProgressPriority): 95 against 99-101 us (per-signal) and 65 against
+    // 67-69 us (shared filter) at 2^25 values.
+    long long left = (tile_end - tile + step - 1) / step;
+    const ProgressPriority priority(left);
+    for (; tile < tile_end; tile += step, --left) {
+        priority.set(left);
         cpx v[4][4];
         if constexpr (kPerSignal) {
             u32x4 z[4];

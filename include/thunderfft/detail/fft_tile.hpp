@@ -379,9 +379,11 @@ struct DirectIO {
 // end; with it a workgroup that gets ahead yields issue slots to those behind.
 // Measured for the VALU-bound fp32 convolutions (conv1d of 16384 signals of
 // 2048 with per-signal filters: 151 against 156-157 us; conv2d of 8192
-// images: 1.5%) and the fp16 conv2d (67.8 against 66.7 us); the MFMA conv1d
-// kernels measured slower with it (real conv1d N = 256: 61.5 against 58 us),
-// so they do not use it.
+// images: 1.5%), the fp16 conv2d (67.8 against 66.7 us) and the fp16 conv1d
+// kernels at N = 2048 and 4096 (1-4%); at N <= 1024 the MFMA conv1d kernels
+// measured neutral or slower with it (real conv1d N = 256: 61.5 against
+// 58 us), and the fp16 C2C kernels slower (N = 2048: 106 against 89 us), so
+// those do not use it.
 // The level is floor((4 left - 1) / total), decided by comparing `left`
 // with three thresholds computed once (left >= ceil((l total + 1) / 4) for
 // level >= l), so a walk pays no division per tile.
