@@ -316,10 +316,12 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
     // At N = 2048 a wave's issue priority falls as its workgroup gets ahead
     // (ProgressPriority): 63.5 against 66-67 us (shared filter) and 91.0
     // against 91.7-92.0 us (per-signal) at 2^25 values; neutral at N <= 1024.
+    // The next tile's level is set after the stores: set at the top of the
+    // loop body, it cost the per-signal kernel 8 more bytes of register spill.
     long long left = (tile_end - tile + step - 1) / step;
     const ProgressPriority priority(left);
-    for (; tile < tile_end; tile += step, --left) {
-        if constexpr (C == 8) priority.set(left);
+    if constexpr (C == 8) priority.set(left);
+    for (; tile < tile_end; tile += step) {
         const int nv = valid(tile);
         const long long off = offset(tile);
         cpx v[kB][4];
@@ -377,6 +379,7 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
                 st_nt(reinterpret_cast<u32x4*>(dst + e),
                       *reinterpret_cast<const u32x4*>(region + P::out_pad(e)));
         }
+        if constexpr (C == 8) priority.set(--left);
     }
 }
 
