@@ -295,7 +295,8 @@ def test_grid_stride_walks(T, n):
     _large_case(T, n, 514 * tile + max(1, tile // 2), directions=(True,))
 
 
-@pytest.mark.parametrize("T,n", [("float", 1024), ("half", 1024), ("half", 4096), ("float", 4096)])
+@pytest.mark.parametrize("T,n", [("float", 1024), ("half", 1024), ("half", 4096), ("float", 4096),
+                                 ("half", 128), ("half", 2048)])
 def test_beyond_2e31_values(T, n):
     """One launch over 2^31 + 5 * 4096 complex values (17 GB per fp32 buffer,
     8.6 GB per fp16 buffer, on a 288 GB device): every signal offset past
