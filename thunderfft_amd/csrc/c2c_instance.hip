@@ -41,6 +41,9 @@ inline Grid make_grid(long long ntiles, int per_cu, int num_cus) {
 //     per workgroup: 188-194 us); with direct movement, same box: 178 / 180 us
 //     against 12 per CU 181 / 179, 8 per CU 184 / 180, 4 per CU 189 / 181,
 //     8 per CU without prefetch 186 / 186, one tile per workgroup 181 / 186.
+//     fp32 N = 2048 as one transform per 128-lane workgroup (each pass
+//     barrier then spans the transform's 2 waves, not 4): 172.6 us at 32
+//     per CU, 180.8 at 16, against 173.3 us (same box).
 //   fp16 N = 2048 (three-stage MFMA, two transforms per tile): 2 per CU with
 //     prefetch 88.2-88.5 us, against 90.6 at 3 per CU and 105.6 without
 //     prefetch (the two-stage one-transform-per-wave kernel it replaced:
