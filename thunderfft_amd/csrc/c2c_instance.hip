@@ -290,7 +290,7 @@ hipError_t launch_conv1d(int precision, bool per_signal_filter, const void* x, c
         enqueue_conv1d<float2, N>(per_signal_filter, g, shape.prefetch,
                                   static_cast<const float2*>(x), static_cast<const float2*>(h),
                                   static_cast<float2*>(y), batch, tw, stream);
-    else
+    else if constexpr (N < 256)  // fp16 N >= 256 returned above (MFMA)
         enqueue_conv1d<__half2, N>(per_signal_filter, g, Prefetch::kNone,
                                    static_cast<const __half2*>(x), static_cast<const __half2*>(h),
                                    static_cast<__half2*>(y), batch, tw, stream);
@@ -351,7 +351,7 @@ hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectr
         conv1d_real_kernel<float2, N, kF32, (N >= 2048)><<<g.blocks, 256, 0, stream>>>(
             static_cast<const float*>(x), spectrum, static_cast<float*>(y), batch, channels, tw,
             g.tiles_per_block);
-    else
+    else if constexpr (N < 256)  // fp16 N >= 256 returned above (MFMA)
         conv1d_real_kernel<__half2, N><<<g.blocks, 256, 0, stream>>>(
             static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch, channels, tw,
             g.tiles_per_block);
