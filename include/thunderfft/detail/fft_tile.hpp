@@ -379,8 +379,9 @@ struct DirectIO {
 // end; with it a workgroup that gets ahead yields issue slots to those behind.
 // Measured for the VALU-bound fp32 convolutions (conv1d of 16384 signals of
 // 2048 with per-signal filters: 151 against 156-157 us; conv2d of 8192
-// images: 1.5%), the fp16 conv2d (67.8 against 66.7 us) and the fp16 conv1d
-// kernels at N = 2048 and 4096 (1-4%); at N <= 1024 the MFMA conv1d kernels
+// images: 1.5%; the valid conv1d: 1.8%) and the fp16 conv1d kernels at
+// N = 2048 and 4096 (1-4%); the fp16 conv2d uses it too, neutral within one
+// box's noise (59.4-61.7 against 60.8 us); at N <= 1024 the MFMA conv1d kernels
 // measured neutral or slower with it (real conv1d N = 256: 61.5 against
 // 58 us), and the fp16 C2C kernels slower (N = 2048: 106 against 89 us), so
 // those do not use it.
