@@ -383,7 +383,8 @@ struct DirectIO {
 // N = 2048 and 4096 (1-4%); the fp16 conv2d uses it too, neutral within one
 // box's noise (59.4-61.7 against 60.8 us); at N <= 1024 the MFMA conv1d kernels
 // measured neutral or slower with it (real conv1d N = 256: 61.5 against
-// 58 us), and the fp16 C2C kernels slower (N = 2048: 106 against 89 us), so
+// 58 us), the fp16 C2C kernels slower (N = 2048: 106 against 89 us) and the
+// fp32 real conv1d neutral or slower (N = 256: 105 against 99-100 us), so
 // those do not use it.
 // The level is floor((4 left - 1) / total), decided by comparing `left`
 // with three thresholds computed once (left >= ceil((l total + 1) / 4) for
