@@ -284,13 +284,32 @@ struct Raw {
     typename Io<IO>::W1 w[16];
 };
 
+// Image img as a buffer resource of its 4096 values: one lane offset serves
+// all 16 accesses of a lane, the 256-element steps go in the scalar offset
+// (cache policy 2: non-temporal).  With 64-bit per-lane pointers instead, the
+// fp32 kernel kept one in scratch at its 128-VGPR budget and reloaded it
+// behind an s_waitcnt vmcnt(0) each image: 96.4 against 97.8-98.4 us for
+// 8192 images.  Every offset stays inside the image (tid * 8 + 15 * 2048 + 8
+// <= 32 KiB), so the resource's bounds never clip an access.
+template <class IO>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t image_rsrc(const IO* base, long long img) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<IO*>(base + img * 4096), 0,
+                                             static_cast<int>(4096 * sizeof(IO)), 0x00020000);
+}
+
 template <class IO>
 __device__ __forceinline__ void load(Raw<IO>& r, const IO* __restrict__ base, long long img,
                                      int tid) {
     using W = typename Io<IO>::W1;
-    const W* p = reinterpret_cast<const W*>(base + img * 4096) + tid;
+    const __amdgpu_buffer_rsrc_t rs = image_rsrc(base, img);
+    const int off = tid * static_cast<int>(sizeof(W));
 #pragma unroll
-    for (int r1 = 0; r1 < 16; ++r1) r.w[r1] = ld_nt(p + 256 * r1);
+    for (int r1 = 0; r1 < 16; ++r1) {
+        if constexpr (sizeof(W) == 8)
+            r.w[r1] = __builtin_bit_cast(W, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 256 * 8 * r1, 2));
+        else
+            r.w[r1] = __builtin_bit_cast(W, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 256 * 4 * r1, 2));
+    }
 }
 
 template <class IO>
@@ -303,17 +322,25 @@ template <class IO>
 __device__ __forceinline__ void store(const cpx (&v)[16], IO* __restrict__ base, long long img,
                                       int tid) {
     using W = typename Io<IO>::W1;
-    W* p = reinterpret_cast<W*>(base + img * 4096) + tid;
+    const __amdgpu_buffer_rsrc_t rs = image_rsrc<IO>(base, img);
+    const int off = tid * static_cast<int>(sizeof(W));
 #pragma unroll
-    for (int r1 = 0; r1 < 16; ++r1) st_nt(p + 256 * r1, Io<IO>::encode1(v[r1]));
+    for (int r1 = 0; r1 < 16; ++r1) {
+        const W w = Io<IO>::encode1(v[r1]);
+        if constexpr (sizeof(W) == 8)
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, w), rs, off, 256 * 8 * r1, 2);
+        else
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, w), rs, off, 256 * 4 * r1, 2);
+    }
 }
 }  // namespace conv2d
 
 // The next image's loads are issued before the current image is transformed.
-// Held to 4 waves per SIMD (4 workgroups per CU): the fp32 kernel then keeps 2
-// dwords in scratch.  Measured on MI355X, 8192 fp32 images: 101-104 us,
-// against 103-106 us at its natural 129 VGPRs (3 per CU) and 104-107 us
-// without the prefetch.
+// Held to 4 waves per SIMD (4 workgroups per CU), which the fp32 kernel fits
+// without spilling since its image accesses are buffer instructions (above).
+// Measured on MI355X, 8192 fp32 images, when it still kept 2 dwords in
+// scratch: 101-104 us, against 103-106 us at its natural 129 VGPRs (3 per CU)
+// and 104-107 us without the prefetch.
 template <class IO>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void
 conv2d64_kernel(const IO* __restrict__ x, const IO* __restrict__ h, IO* __restrict__ y,

@@ -262,7 +262,7 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
         wave_lds_sync();
 #pragma unroll
         for (int i = 0; i < kRaw; ++i)
-            *reinterpret_cast<u32x4*>(region + P::in_pad(4 * lane + 256 * i)) = raw[i];
+            *reinterpret_cast<u32x4*>(region + P::in_pad(4 * lane) + P::kInStep * i) = raw[i];
         wave_lds_sync();
     };
     auto forward = [&](cpx (&v)[kB][4]) {
@@ -371,13 +371,17 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
                 region[P::out_pad((b / C) * N + n + 16 * (b % C) + P::kM * (q + 4 * r))] =
                     pack_half2({v[b][r].re, -v[b][r].im});
         wave_lds_sync();
+        // The staging addresses as one base and constant steps: computed per
+        // piece, they kept enough registers live to spill one (8 bytes per
+        // lane, reloaded among the stores at N = 2048).
         __half2* dst = y + off;
+        const unsigned* const obase = region + P::out_pad(4 * lane);
 #pragma unroll
         for (int i = 0; i < kRaw; ++i) {
             const int e = 4 * lane + 256 * i;
             if (e < nv)
                 st_nt(reinterpret_cast<u32x4*>(dst + e),
-                      *reinterpret_cast<const u32x4*>(region + P::out_pad(e)));
+                      *reinterpret_cast<const u32x4*>(obase + P::kOutStep * i));
         }
         if constexpr (C == 8) priority.set(--left);
     }

@@ -149,6 +149,11 @@ struct MfmaPlan {
     static constexpr int kTw1 = C * 4 * 64;        // first twiddles, [c][r][lane]
     static constexpr int kA3 = (C > 1 ? C - 1 : 1) * 2 * 64;  // folded stage-3 operands (u32x4)
     __device__ static __forceinline__ int in_pad(int k) { return k + kInPad * (k / kInPeriod); }
+    // Padded offsets of the 16-byte staging pieces e = 4 l + 256 i of lane l:
+    // both pad periods divide 256, so piece i sits a constant step past piece 0.
+    static constexpr int kInStep = 256 + kInPad * (256 / kInPeriod);
+    static constexpr int kOutStep = 256 + kOutPad * (256 / kOutPeriod);
+    static_assert(256 % kInPeriod == 0 && 256 % kOutPeriod == 0, "constant staging steps");
     __device__ static __forceinline__ int out_pad(int k) {
         return k + kOutPad * (k / kOutPeriod);
     }
