@@ -277,3 +277,45 @@ def test_beyond_2e31_samples(T):
         assert rel <= 1e-3 and worst <= 5e-3
     del d_x, d_y
     torch.cuda.empty_cache()
+
+
+def test_n4096_many_channels_odd_batch():
+    """fp16 N = 4096 with 262145 channels: row 1 of a pair lies D N = 2^30 + 4096
+    values past row 0, so the row offsets pass 2^31 bytes within one pair.
+    Odd batch (3): the second pair has no row 1.  Channel d's filter is a
+    unit impulse at (17 d + 1) mod N, so each output row is its input row
+    rolled; checked on rows of every batch index at spread channels, the
+    first and the last."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    n, channels, batch = 4096, 262145, 3
+    assert 2 * (channels + 1) * n > 2**31 - 1
+    thff.ThunderFFTInitialize("half", n)
+    shifts = (17 * torch.arange(channels, device="cuda") + 1) % n
+    d_h = torch.zeros(channels, n, dtype=torch.float32, device="cuda")
+    d_h[torch.arange(channels, device="cuda"), shifts] = 1.0
+    d_spec = torch.empty(channels, n, 2, dtype=torch.float32, device="cuda")
+    thff.ThunderFFT_conv1d_real_filter("half", n, d_h, d_spec, channels, 1.0 / n)
+    del d_h
+    rows_total = batch * channels
+    d_x = torch.empty(rows_total * n, dtype=torch.float16, device="cuda")
+    d_x.uniform_(-1, 1)
+    d_y = torch.full_like(d_x, float("nan"))
+    thff.ThunderFFT_conv1d_real("half", n, d_x, d_spec, d_y, batch, channels)
+    chans = torch.tensor([0, 1, 2, 131072, 262143, 262144], device="cuda")
+    rows = (torch.arange(batch, device="cuda")[:, None] * channels + chans[None, :]).reshape(-1)
+    xs = d_x.view(rows_total, n).index_select(0, rows).float()
+    ys = d_y.view(rows_total, n).index_select(0, rows).float()
+    s = shifts[rows % channels]
+    idx = (torch.arange(n, device="cuda")[None, :] - s[:, None]) % n
+    want = torch.gather(xs, 1, idx)
+    assert bool(torch.isfinite(ys).all())
+    rel = float(torch.linalg.vector_norm(ys - want) / torch.linalg.vector_norm(want))
+    worst = float((ys - want).abs().max())
+    print(f"half real conv N={n} channels={channels} batch={batch}: rel_l2={rel:.3e} "
+          f"max={worst:.3e}", flush=True)
+    assert rel <= 1e-3 and worst <= 5e-3
+    del d_x, d_y, d_spec
+    torch.cuda.empty_cache()
