@@ -1037,11 +1037,6 @@ __device__ __forceinline__ int fx_addr(int kr, int c) {
 }
 __device__ __forceinline__ int rm_addr(int r, int c) { return r * kStride + c; }
 
-__device__ __forceinline__ cpx unpack_half2(unsigned w) {
-    const float2 f = __half22float2(__builtin_bit_cast(__half2, w));
-    return {f.x, f.y};
-}
-
 // DFT4 over the block index of v[b][t] for every t (in-lane), forward.
 __device__ __forceinline__ void dft4_blocks(cpx (&v)[4][4]) {
 #pragma unroll

@@ -122,6 +122,11 @@ __device__ __forceinline__ unsigned pack_half2(cpx v) {
     return __builtin_bit_cast(unsigned, __floats2half2_rn(v.re, v.im));
 }
 
+__device__ __forceinline__ cpx unpack_half2(unsigned w) {
+    const float2 f = __half22float2(__builtin_bit_cast(__half2, w));
+    return {f.x, f.y};
+}
+
 __device__ __forceinline__ f16x8 as_f16x8(u32x4 w) { return __builtin_bit_cast(f16x8, w); }
 
 // Plan of the MFMA kernel for N = 256*C = 16 x (C x 16), C in {1, 2, 4, 8}.
@@ -408,6 +413,11 @@ struct MfmaCoeffs {
     f16x8 a_in[2], a[2];
     cpx w1[C * 4];
     cpx w2[C > 1 ? C - 1 : 1];
+    // Uniform views for the device API's packed form: operand register i
+    // (a_in, then a) and twiddle i (w1, then the w2 in use).
+    static constexpr int kTwiddles = 4 * C + C - 1;
+    __device__ __forceinline__ f16x8& op(int i) { return i < 2 ? a_in[i] : a[i - 2]; }
+    __device__ __forceinline__ cpx& twiddle(int i) { return i < 4 * C ? w1[i] : w2[i - 4 * C]; }
 
     template <bool FWD, class Tw>
     __device__ __forceinline__ void fill(int lane, Tw tw_at) {
@@ -626,6 +636,9 @@ struct Mfma4096Coeffs {
     static constexpr int N = 4096;
     f16x8 a[2], a_in[2];
     cpx w1[4][4], w2[4];
+    static constexpr int kTwiddles = 20;
+    __device__ __forceinline__ f16x8& op(int i) { return i < 2 ? a[i] : a_in[i - 2]; }
+    __device__ __forceinline__ cpx& twiddle(int i) { return i < 16 ? w1[i >> 2][i & 3] : w2[i - 16]; }
 
     template <bool FWD, class Tw>
     __device__ __forceinline__ void fill(int tid, Tw tw_at) {
@@ -1061,6 +1074,9 @@ struct Mfma2048Coeffs {
     static constexpr int N = 2048;
     f16x8 a8[2], a[2];
     cpx w1[4][4], w2[4];
+    static constexpr int kTwiddles = 20;
+    __device__ __forceinline__ f16x8& op(int i) { return i < 2 ? a8[i] : a[i - 2]; }
+    __device__ __forceinline__ cpx& twiddle(int i) { return i < 16 ? w1[i >> 2][i & 3] : w2[i - 16]; }
 
     template <bool FWD, class Tw>
     __device__ __forceinline__ void fill(int tid, Tw tw_at) {

@@ -65,9 +65,12 @@ int thff_finalize(int precision);
  *   unsupported precision or n -> THFF_EINVAL (a static_assert there);
  *   batch < 0 -> THFF_EINVAL; batch == 0 -> THFF_OK without touching the
  *   pointers; null d_input or d_output, or d_input == d_output -> THFF_EINVAL;
- *   a buffer not on a 16-byte boundary -> THFF_EINVAL (the kernels move
- *   16-byte vectors; the reference has no such check, and any hipMalloc'd
- *   pointer or offset of whole transforms meets it).
+ *   a buffer not aligned to its element (8 bytes for float2, 4 bytes for
+ *   half2) -> THFF_EINVAL, since no kernel can read a split element.
+ * Any element-aligned buffer is accepted, as in the reference: buffers on a
+ * 16-byte boundary (every hipMalloc pointer, and every offset of whole
+ * transforms of >= 2 values) take the vectorised kernels; others take a
+ * kernel that moves single elements.
  * Requires thff_initialize(precision, n) on the current device (THFF_EIO
  * otherwise).  Synchronises `stream` before returning, like the reference. */
 int thff_global(int precision, int n, int forward, const void* d_input, void* d_output,
@@ -90,8 +93,11 @@ int thff_global_async(int precision, int n, int forward, const void* d_input, vo
  * pointwise product, inverse FFT and the 1/n scale; the spectra stay on chip).
  * x and y hold batch*n complex values, h holds batch*n (per-signal) or n
  * (shared) values, all in `precision` storage, natural order.  Same checks and
- * return codes as thff_global (y may alias neither x nor h), requires
- * thff_initialize(precision, n), synchronises `stream` before returning. */
+ * return codes as thff_global (y may alias neither x nor h), except that x, h
+ * and y must start on a 16-byte boundary (THFF_EINVAL otherwise: the fused
+ * kernels move 16-byte vectors only; every offset of whole signals meets it).
+ * Requires thff_initialize(precision, n), synchronises `stream` before
+ * returning. */
 int thff_conv1d(int precision, int n, const void* d_x, const void* d_h, void* d_y, int batch,
                 int per_signal_filter, void* stream);
 

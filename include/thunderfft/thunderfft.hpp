@@ -85,9 +85,11 @@ inline const float2* ThunderFFT_twiddle_table() {
 
 // Batched unnormalized out-of-place C2C FFT of `batch` natural-order signals
 // of N values (signal j at offset j*N).  forward = exp(-2*pi*i*k/N).
-// batch < 0, null, identical or not 16-byte aligned pointers throw
-// std::invalid_argument; batch 0
-// is a no-op.  Synchronises `stream` before returning.
+// batch < 0, null or identical pointers, and pointers not aligned to their
+// element (8 bytes for float2, 4 for half2) throw std::invalid_argument;
+// batch 0 is a no-op.  Any element-aligned buffer is accepted, as in the
+// reference; 16-byte aligned ones take the vectorised kernels.  Synchronises
+// `stream` before returning.
 template <typename T, int N, bool forward = true>
 inline void ThunderFFT_global(vec2_t<T>* d_input, vec2_t<T>* d_output, int batch,
                               hipStream_t stream = 0) {

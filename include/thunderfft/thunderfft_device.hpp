@@ -39,9 +39,10 @@
 //    ThunderFFT_kernel_reg, which then loads the lane's factors itself.  For
 //    half, as in the reference's fused samples, a kernel can instead build
 //    its coefficients once with unit_fp16::make_reg_b_precompute<N, fwd>(W)
-//    (vec2_t<half> W[unit_fp16::coefficient_count<N>]; no table needed) and
+//    (vec2_t<half> W[36], or W[28] for N <= 128, the reference's sizes;
+//    unit_fp16::coefficient_count<N> is never more; no table needed) and
 //    pass W to ThunderFFT_kernel_reg: the MFMA transforms then build no
-//    operand and read no twiddle per call.
+//    operand and read no twiddle table per call.
 //  * layout_t::Reversed on an input layout selects the permutation the
 //    transforms expect, which here is the identity (natural order).
 #pragma once
@@ -263,9 +264,9 @@ __device__ __forceinline__ void ThunderFFT_kernel_reg(vec2_t<T>* __restrict__ re
 
 namespace detail {
 
-// The per-lane coefficients of the fp16 transform of length N: the MFMA
-// transforms' operands and twiddles (N = 256 ... 4096) or the VALU passes'
-// twiddle factors (N = 64, 128).
+// The per-lane coefficients of the fp16 transform of length N in fp32 form:
+// the MFMA transforms' operands and twiddles (N = 256 ... 4096) or the VALU
+// passes' twiddle factors (N = 64, 128).
 template <int N>
 using half_coefficients = std::conditional_t<
     N == 4096, thff::Mfma4096Coeffs,
@@ -273,18 +274,61 @@ using half_coefficients = std::conditional_t<
     std::conditional_t<fragment_on_mfma<half, N>, thff::MfmaCoeffs<(N >= 256 ? N / 256 : 1)>,
                        thff::LaneTwiddles<N>>>>;
 
+// The reference's slot budget for those coefficients: make_reg_b_precompute
+// fills 28 half2 for N = 64, 128 and 36 for N = 256 ... 4096
+// (unit_kernel_fp16.cuh:97-108), and its fused kernels declare arrays of
+// exactly that size (sample/conv1d/main.cu:61, conv1d_fullfft_l4096_thunder.cu
+// :298, sample/conv2d/thunder.cu:84,125).
+template <int N>
+inline constexpr int reference_coefficient_slots = N <= 128 ? 28 : 36;
+
+// An MFMA transform's coefficients with every twiddle held as one f16 pair
+// (real low, imaginary high), rounded once, and the DFT16 operands (f16
+// already) as they are: at N = 1024 (19 twiddles) and 2048, 4096 (20) the
+// fp32 form needs 56 slots, this one 36.  The f16 twiddle adds an error of
+// the size of the f16 rounding the data already takes before every DFT16.
+template <class Full>
+struct PackedMfmaCoefficients {
+    thff::f16x8 ops[4];
+    unsigned tw[Full::kTwiddles];
+    __device__ __forceinline__ void pack(Full& k) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ops[i] = k.op(i);
+#pragma unroll
+        for (int i = 0; i < Full::kTwiddles; ++i) tw[i] = thff::pack_half2(k.twiddle(i));
+    }
+    __device__ __forceinline__ void unpack(Full& k) const {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) k.op(i) = ops[i];
+#pragma unroll
+        for (int i = 0; i < Full::kTwiddles; ++i) k.twiddle(i) = thff::unpack_half2(tw[i]);
+    }
+};
+
+// What make_reg_b_precompute<N, fwd> stores in W: the fp32 form where it fits
+// the reference's budget (N = 64 ... 512), else the packed one.
+template <int N>
+using half_coefficient_slots = std::conditional_t<
+    sizeof(half_coefficients<N>) <= sizeof(unsigned) * reference_coefficient_slots<N>,
+    half_coefficients<N>, PackedMfmaCoefficients<half_coefficients<N>>>;
+
+template <int N>
+inline constexpr bool half_coefficients_packed =
+    !std::is_same_v<half_coefficient_slots<N>, half_coefficients<N>>;
+
 }  // namespace detail
 
 namespace unit_fp16 {
 
 // half2 slots of per-lane coefficients that make_reg_b_precompute<N, fwd>
 // writes and ThunderFFT_kernel_reg<half, N, batch, fwd>(reg, W, workspace)
-// reads (a slot holds 32 bits: f16 operand pairs or one fp32 twiddle
-// component).  The reference's arrays are 28 or 36 half2 (unit_kernel_fp16.cuh
-// :97-108); declare W[coefficient_count<N>] instead.
+// reads (a slot holds 32 bits: f16 operand pairs, an f16 twiddle pair or one
+// fp32 twiddle component).  Never more than the reference's 28 (N <= 128) or
+// 36 (N >= 256) half2 (unit_kernel_fp16.cuh:97-108): a kernel written for the
+// reference keeps its W_fwd[36] / W_inv[36] arrays.
 template <int N>
 inline constexpr int coefficient_count =
-    static_cast<int>(sizeof(detail::half_coefficients<N>) / sizeof(unsigned));
+    static_cast<int>(sizeof(detail::half_coefficient_slots<N>) / sizeof(unsigned));
 
 // This lane's coefficients of the fp16 transform of length N in direction
 // `forward` (the reference's unit_fp16::make_reg_b_precompute<N, fwd>,
@@ -293,16 +337,18 @@ inline constexpr int coefficient_count =
 // transcendentals (no table, no memory access; their error is far below the
 // f16 rounding of the data), once per kernel.  Call with the same block
 // shape and lane numbering as ThunderFFT_kernel_reg.  W is a vec2_t<half>
-// array or pointer; an array is checked at compile time to hold
-// coefficient_count<N> slots (the reference's kernels declare 28 or 36,
-// fewer than the MFMA transforms at N = 1024 and 4096 need).
+// array or pointer to at least coefficient_count<N> slots, which is at most
+// the reference's 28 / 36; an array is checked at compile time.
 template <int N, bool forward, class Coeffs>
 __device__ __forceinline__ void make_reg_b_precompute(Coeffs&& W_arg) {
+    static_assert(coefficient_count<N> <= detail::reference_coefficient_slots<N>,
+                  "the coefficients must fit the reference's W arrays");
     using A = std::remove_reference_t<Coeffs>;
     if constexpr (std::is_array_v<A>)
         static_assert(std::extent_v<A> >= static_cast<size_t>(coefficient_count<N>),
                       "make_reg_b_precompute: declare vec2_t<half> "
-                      "W[thunderfft::unit_fp16::coefficient_count<N>]");
+                      "W[thunderfft::unit_fp16::coefficient_count<N>] (28 for N <= 128, "
+                      "36 otherwise, as in the reference)");
     vec2_t<half>* const W = W_arg;
     detail::check_shape<N, batch_per_block<N>>();
     const int tid = detail::block_tid();
@@ -313,7 +359,13 @@ __device__ __forceinline__ void make_reg_b_precompute(Coeffs&& W_arg) {
         k.template build<forward>(tid & 63);
     else
         k.build(tid % (N / 16));
-    __builtin_memcpy(static_cast<void*>(W), &k, sizeof(k));
+    if constexpr (detail::half_coefficients_packed<N>) {
+        detail::half_coefficient_slots<N> packed;
+        packed.pack(k);
+        __builtin_memcpy(static_cast<void*>(W), &packed, sizeof(packed));
+    } else {
+        __builtin_memcpy(static_cast<void*>(W), &k, sizeof(k));
+    }
 }
 
 }  // namespace unit_fp16
@@ -332,7 +384,13 @@ __device__ __forceinline__ void ThunderFFT_kernel_reg(vec2_t<T>* __restrict__ re
         detail::check_shape<N, batch>();
         const int tid = detail::block_tid();
         detail::half_coefficients<N> k;
-        __builtin_memcpy(&k, static_cast<const void*>(W), sizeof(k));
+        if constexpr (detail::half_coefficients_packed<N>) {
+            detail::half_coefficient_slots<N> packed;
+            __builtin_memcpy(&packed, static_cast<const void*>(W), sizeof(packed));
+            packed.unpack(k);
+        } else {
+            __builtin_memcpy(&k, static_cast<const void*>(W), sizeof(k));
+        }
         if constexpr (N == 4096) {
             thff::cpx y[4][4];
 #pragma unroll

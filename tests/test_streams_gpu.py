@@ -130,6 +130,7 @@ def test_initialize_races_transforms_on_another_thread():
     bit-exact result of an undisturbed call or fails with the documented
     missing-table error; none crashes or reads a freed table."""
     import threading
+    import time
 
     import torch
 
@@ -147,41 +148,54 @@ def test_initialize_races_transforms_on_another_thread():
 
     stream = torch.cuda.Stream()
     outcome = {"ok": 0, "missing": 0, "mismatch": 0, "other": [], "switches": 0}
-    start = threading.Barrier(2)
+    start = threading.Barrier(2, timeout=60)
     done = threading.Event()
+    errors = []  # exceptions raised in the worker threads, re-raised below
 
     def transforms():
-        d_y = torch.empty_like(d_x)
-        start.wait()
-        for _ in range(calls):
-            d_y.fill_(float("nan"))
-            torch.cuda.synchronize()
-            try:
-                thff.ThunderFFT_global("float", n, True, d_x, d_y, batch, stream)
-            except RuntimeError as e:
-                if "ThunderFFTInitialize" in str(e):
-                    outcome["missing"] += 1
+        try:
+            d_y = torch.empty_like(d_x)
+            start.wait()
+            for _ in range(calls):
+                d_y.fill_(float("nan"))
+                torch.cuda.synchronize()
+                try:
+                    thff.ThunderFFT_global("float", n, True, d_x, d_y, batch, stream)
+                except RuntimeError as e:
+                    if "ThunderFFTInitialize" in str(e):
+                        outcome["missing"] += 1
+                    else:
+                        outcome["other"].append(str(e))
+                    continue
+                if torch.equal(d_y, d_ref):
+                    outcome["ok"] += 1
                 else:
-                    outcome["other"].append(str(e))
-                continue
-            if torch.equal(d_y, d_ref):
-                outcome["ok"] += 1
-            else:
-                outcome["mismatch"] += 1
-        done.set()
+                    outcome["mismatch"] += 1
+        except BaseException as e:  # noqa: BLE001 - reported in the main thread
+            errors.append(e)
+        finally:
+            done.set()  # the toggling thread stops whatever happened here
 
     def switches():
-        start.wait()
-        while not done.is_set():  # toggle for as long as the transforms run
-            thff.ThunderFFTInitialize("float", 512)
-            thff.ThunderFFTInitialize("float", n)
-            outcome["switches"] += 1
+        deadline = time.monotonic() + 90  # bounded even if `done` were never set
+        try:
+            start.wait()
+            while not done.is_set() and time.monotonic() < deadline:
+                thff.ThunderFFTInitialize("float", 512)
+                thff.ThunderFFTInitialize("float", n)
+                outcome["switches"] += 1
+        except BaseException as e:  # noqa: BLE001
+            errors.append(e)
+            done.set()
 
     workers = [threading.Thread(target=transforms), threading.Thread(target=switches)]
     for w in workers:
         w.start()
     for w in workers:
-        w.join()
+        w.join(timeout=120)
+    assert not any(w.is_alive() for w in workers), "a worker thread did not finish"
+    if errors:
+        raise errors[0]
     print(f"initialize race: {outcome}", flush=True)
     assert outcome["mismatch"] == 0 and not outcome["other"], outcome
     assert outcome["ok"] + outcome["missing"] == calls, outcome

@@ -108,11 +108,13 @@ __global__ __launch_bounds__(256) void fused_filter(const vec2_t<T>* in, vec2_t<
 }
 
 // The coefficient argument of ThunderFFT_kernel_reg(reg, W, ws) in the
-// reference's types: half -> this lane's precomputed coefficients, float ->
-// the table.
+// reference's types: half -> this lane's precomputed coefficients in an
+// array of the size the reference's fused kernels declare (W_fwd[28] for
+// N <= 128, sample/conv1d/main.cu:61; W_fwd[36] otherwise,
+// conv1d_fullfft_l4096_thunder.cu:298), float -> the table.
 template <class T, int N, bool FWD>
 struct KernelRegW {
-    vec2_t<T> coeffs[std::is_same_v<T, half> ? thunderfft::unit_fp16::coefficient_count<N> : 1];
+    vec2_t<T> coeffs[std::is_same_v<T, half> ? (N <= 128 ? 28 : 36) : 1];
     vec2_t<T>* w;
     __device__ explicit KernelRegW(const float2* tw) {
         if constexpr (std::is_same_v<T, half>) {

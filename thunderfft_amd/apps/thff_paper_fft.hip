@@ -98,7 +98,7 @@ __global__ __launch_bounds__(256) void repeat_kernel(const vec2_t<T>* __restrict
     // coefficients of unit_fp16::make_reg_b_precompute, built once here as
     // in the reference's fused samples (sample/README.md:406-409).
     thunderfft::lane_twiddles<N> tw_lane;
-    vec2_t<T> coeffs[std::is_same_v<T, half> ? thunderfft::unit_fp16::coefficient_count<N> : 1];
+    vec2_t<T> coeffs[std::is_same_v<T, half> ? (N <= 128 ? 28 : 36) : 1];  // the reference's sizes
     if constexpr (std::is_same_v<T, half>)
         thunderfft::unit_fp16::make_reg_b_precompute<N, true>(coeffs);
     else
