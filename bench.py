@@ -155,10 +155,14 @@ def time_gpu(T: str, forward: bool, steps: int, warmup: int, n: int = N_FFT,
     }
 
 
-def time_conv(kind: str, T: str, steps: int, warmup: int) -> dict:
+def time_conv(kind: str, T: str, steps: int, warmup: int, size: int = 64,
+              images: int = 8192) -> dict:
     """One of the fused convolution workloads: conv1d (16384 signals of 2048,
-    per-signal complex filters with N(0, 1/sqrt(2048)) taps) or conv2d (8192
-    64 x 64 images, one shared real filter with a N(0, 1/7) 7 x 7 corner block)."""
+    per-signal complex filters with N(0, 1/sqrt(2048)) taps) or conv2d (`images`
+    size x size images, one shared real filter with a N(0, 1/7) 7 x 7 corner
+    block: 8192 of 64 x 64 is config 5; 2048 of 128 x 128 and 32 of 1024 x 1024
+    move the same 2^25 values; 1 of 1024 x 1024 is the reference sample's
+    shape, sample/conv2d/thunder.cu:556-565)."""
     import numpy as np
     import torch
 
@@ -175,14 +179,16 @@ def time_conv(kind: str, T: str, steps: int, warmup: int) -> dict:
         flops = 3 * 5.0 * n * math.log2(n) * batch + 6.0 * count
         init_n = n
     else:
-        n, batch = 4096, 8192
+        n, batch = size * size, images
         count = n * batch
-        hh = np.zeros((64, 64, 2), dtype=np.float32)
+        hh = np.zeros((size, size, 2), dtype=np.float32)
         hh[:7, :7, 0] = np.random.default_rng(7).normal(0.0, 1.0 / 7.0, (7, 7))
         h = torch.from_numpy(hh.reshape(-1)).to(device="cuda", dtype=dt)
         nbytes = 2 * count * elem
-        flops = 2 * 2 * 64 * 5.0 * 64 * math.log2(64) * batch + 6.0 * count
-        init_n = 64
+        flops = 2 * 2 * size * 5.0 * size * math.log2(size) * batch + 6.0 * count
+        if size == 1024:  # the filter's spectrum is computed in every call
+            flops += 2 * size * 5.0 * size * math.log2(size)
+        init_n = size
     x = torch.empty(2 * count, dtype=dt, device="cuda")
     y = torch.empty_like(x)
     stream = torch.cuda.current_stream()
@@ -193,13 +199,15 @@ def time_conv(kind: str, T: str, steps: int, warmup: int) -> dict:
         if kind == "conv1d":
             thff.ThunderFFT_conv1d_async(T, n, x, h, y, batch, True, stream)
         else:
-            thff.ThunderFFT_conv2d_async(T, 64, 64, x, h, y, batch, stream)
+            thff.ThunderFFT_conv2d_async(T, size, size, x, h, y, batch, stream)
 
     ms = timed(launch, steps, warmup, stream)
     thff.ThunderFFTFinalize(T)
     del x, y, h
-    return {"workload": (f"{kind} {batch} x {'2048' if kind == 'conv1d' else '64x64'} "
-                         f"{T}2, fused FFT * H * IFFT"),
+    shape = "2048" if kind == "conv1d" else f"{size}x{size}"
+    how = ("row pass, fused column FFT * H * IFFT, inverse row pass (filter spectrum in the call)"
+           if kind == "conv2d" and size == 1024 else "fused FFT * H * IFFT")
+    return {"workload": f"{kind} {batch} x {shape} {T}2, {how}",
             "precision": T, "us_per_call": ms * 1e3, "median_us_per_call": LAST_MEDIAN_MS * 1e3,
             "gflops": flops / (ms * 1e-3) / 1e9,
             "gbps": nbytes / (ms * 1e-3) / 1e9,
@@ -207,12 +215,14 @@ def time_conv(kind: str, T: str, steps: int, warmup: int) -> dict:
             "bytes_per_call": nbytes}
 
 
-def time_conv_real(T: str, n: int, steps: int, warmup: int) -> dict:
+def time_conv_real(T: str, n: int, steps: int, warmup: int, with_filter: bool = False) -> dict:
     """The reference's real-input fused convolution
     (sample/conv1d/conv1d_fullfft_l4096_thunder.cu:280-331) at 2^26 real samples:
     16384 signals [B=16384*4096/(n*64)][D=64][n], one real 9-tap filter per
-    channel (the sample's default K) whose spectra are prepared once outside
-    the timed region (its include_filter_fft=0 mode)."""
+    channel (the sample's default K).  By default the spectra are prepared
+    once outside the timed region (its include_filter_fft=0 mode); with
+    with_filter every timed step prepares them first (the sample's default,
+    include_filter_fft=1, :481,582)."""
     import torch
 
     import thunderfft_amd as thff
@@ -233,6 +243,8 @@ def time_conv_real(T: str, n: int, steps: int, warmup: int) -> dict:
     thff.ThunderFFT_conv1d_real_filter(T, n, h, spectrum, channels, 1.0, stream)
 
     def launch():
+        if with_filter:
+            thff.ThunderFFT_conv1d_real_filter_async(T, n, h, spectrum, channels, 1.0, stream)
         thff.ThunderFFT_conv1d_real_async(T, n, x, spectrum, y, batch, channels, stream)
 
     ms = timed(launch, steps, warmup, stream)
@@ -240,9 +252,13 @@ def time_conv_real(T: str, n: int, steps: int, warmup: int) -> dict:
     nbytes = 2 * count * elem  # x and y; the spectra (2 MiB) stay in L2
     transforms = count // (2 * n)  # two real signals per complex transform
     flops = transforms * (2 * 5.0 * n * math.log2(n) + 6.0 * n)
+    if with_filter:
+        flops += channels * 5.0 * n * math.log2(n)
     del x, y, h, spectrum
+    prep = ("spectra prepared in every step (include_filter_fft=1)" if with_filter
+            else "spectra prepared once")
     return {"workload": (f"conv1d_real [{batch}][{channels}][{n}] {T}, 9-tap real filters, "
-                         f"fused FFT * H * IFFT (two signals per complex transform)"),
+                         f"fused FFT * H * IFFT (two signals per complex transform), {prep}"),
             "precision": T, "us_per_call": ms * 1e3, "median_us_per_call": LAST_MEDIAN_MS * 1e3,
             "gflops": flops / (ms * 1e-3) / 1e9,
             "gbps": nbytes / (ms * 1e-3) / 1e9,
@@ -639,6 +655,20 @@ def main():
         print(f"[bench] {r['workload']}: {r['us_per_call']:.1f} us, {r['gbps']:.0f} GB/s "
               f"({r['pct_hbm_peak']:.1f}% of HBM peak), {r['gflops']:.0f} GFLOP/s",
               file=sys.stderr, flush=True)
+    for size, images, key in ((128, 2048, "conv2d128"), (1024, 32, "conv2d1024"),
+                              (1024, 1, "conv2d1024_single")):
+        for T in ("float", "half"):
+            r = time_conv("conv2d", T, max(1, a.steps // 2), max(1, a.warmup // 2), size, images)
+            runs[f"{key}_{T}"] = r
+            print(f"[bench] {r['workload']}: {r['us_per_call']:.1f} us, {r['gbps']:.0f} GB/s "
+                  f"({r['pct_hbm_peak']:.1f}% of HBM peak), {r['gflops']:.0f} GFLOP/s",
+                  file=sys.stderr, flush=True)
+    for T, n in (("half", 4096),):
+        r = time_conv_real(T, n, max(1, a.steps // 2), max(1, a.warmup // 2), with_filter=True)
+        runs[f"conv1d_real_{T}_n{n}_with_filter"] = r
+        print(f"[bench] {r['workload']}: {r['us_per_call']:.1f} us, {r['gbps']:.0f} GB/s "
+              f"({r['pct_hbm_peak']:.1f}% of HBM peak), {r['gflops']:.0f} GFLOP/s",
+              file=sys.stderr, flush=True)
     for T, n in (("half", 4096), ("half", 1024), ("half", 256), ("float", 4096)):
         r = time_conv_real(T, n, max(1, a.steps // 2), max(1, a.warmup // 2))
         runs[f"conv1d_real_{T}_n{n}"] = r
@@ -724,8 +754,11 @@ def main():
         if util is not None:
             out["also"][k]["mfma_util_pct"] = util
     out["also"]["conv_note"] = ("conv1d bytes = x, h and y (3 * 2^25 complex); conv2d bytes = x "
-                                "and y (2 * 2^25 complex; the 32 KiB filter is read per "
-                                "workgroup from L2); conv1d_real bytes = x and y (2 * 2^26 "
+                                "and y (2 * images * rows * cols complex: 2^25 per array except "
+                                "the single 1024 x 1024 image; the filter is read per workgroup "
+                                "from L2 at 64 and 128, and its spectrum is computed in every "
+                                "1024 x 1024 call, whose intermediate passes are not counted); "
+                                "conv1d_real bytes = x and y (2 * 2^26 "
                                 "real samples); conv1d_valid bytes = x and y (2^26 + 2^26 - F + 1 "
                                 "complex); GFLOP/s counts 5 N log2 N per transform")
     print(json.dumps(out), flush=True)

@@ -380,6 +380,330 @@ conv2d64_kernel(const IO* __restrict__ x, const IO* __restrict__ h, IO* __restri
 }
 
 // ---------------------------------------------------------------------------
+// 2-D circular convolution of 128 x 128 images with one shared filter (the
+// contract of conv2d64_kernel; the reference's 128-tile sketch is
+// sample/conv2d/thunder_tile128.cu:64-237): one image per workgroup of 1024
+// lanes (16 waves), the image held in LDS in fp32, row-major, element (r, c)
+// at r * kStride + lds_pad(c) (140 KiB, so one workgroup per CU):
+//   rows:    wave w owns rows 8 w .. 8 w + 7; lane (r, t) = (8 w + l / 8, l % 8)
+//            holds x[r][t + 8 j], j < 16, and runs the length-128 transform
+//            with the row itself as its slot (wave-scope syncs only);
+//   barrier;
+//   columns: lane (c, t) = (tid / 8, tid % 8) transforms column c where it
+//            lies (StridedSlot, stride kStride; the 8 lanes of a column are
+//            one wave's, so again wave-scope syncs only): forward, times the
+//            filter spectrum / 16384 (fp32 registers, same layout), inverse;
+//   barrier;
+//   rows:    the inverse row transforms, out.
+// Each wave moves its own 8 rows (8 KiB fp32, 4 KiB half) between HBM and LDS
+// in 16-byte pieces, so staging needs no workgroup barrier: two barriers per
+// image.  The next image's pieces are loaded before the current image is
+// transformed.  kStride = 140 (2 * 140 = 24 mod 64 banks) keeps the column
+// reads of a half-wave (8 rows t + 8 j by 4 columns) on distinct banks.
+// The filter spectrum is computed per workgroup at set-up, as the first half
+// of an image.
+// ---------------------------------------------------------------------------
+namespace conv2d128 {
+inline constexpr int kN = 128;
+inline constexpr int kStride = 140;
+inline constexpr int kLds = kN * kStride;  // cpx
+inline constexpr int kLanes = 1024;
+
+template <class IO>
+struct Pieces {
+    static constexpr int kVec = Io<IO>::kVec;
+    static constexpr int kCount = 1024 / (64 * kVec);  // 16-byte pieces per lane (8 / 4)
+    typename Io<IO>::W4 w[kCount];
+};
+
+// Pieces [First, Last) of the wave's 8 rows of image img: piece i holds
+// values 1024 w + kVec l + 64 kVec i.
+template <int First, int Last, class IO>
+__device__ __forceinline__ void load(Pieces<IO>& p, const IO* __restrict__ base, long long img,
+                                     int wave, int lane) {
+    using W = typename Io<IO>::W4;
+    const IO* src = base + img * (kN * kN) + 1024 * wave + Pieces<IO>::kVec * lane;
+#pragma unroll
+    for (int i = First; i < Last; ++i)
+        p.w[i] = ld_nt(reinterpret_cast<const W*>(src + 64 * Pieces<IO>::kVec * i));
+}
+
+// Pieces of the next image loaded before the current one is transformed (the
+// rest right after its store): with the image (32 VGPRs) and its filter
+// spectrum (32) live, two pieces fit the 128 VGPRs of 4 waves per SIMD
+// without spilling in both types (three spill 8 bytes).
+template <class IO>
+inline constexpr int kEarly = 2;
+
+template <class IO>
+__device__ __forceinline__ void stage(const Pieces<IO>& p, cpx* lds, int wave, int lane) {
+    constexpr int kVec = Pieces<IO>::kVec;
+#pragma unroll
+    for (int i = 0; i < Pieces<IO>::kCount; ++i) {
+        const int e = 1024 * wave + kVec * lane + 64 * kVec * i;  // image value
+        cpx q[kVec];
+        Io<IO>::decode4(p.w[i], q);
+#pragma unroll
+        for (int c = 0; c < kVec; ++c) lds[(e >> 7) * kStride + lds_pad((e & 127) + c)] = q[c];
+    }
+}
+
+template <class IO>
+__device__ __forceinline__ void store(IO* __restrict__ base, long long img, const cpx* lds,
+                                      int wave, int lane) {
+    using W = typename Io<IO>::W4;
+    constexpr int kVec = Pieces<IO>::kVec;
+    IO* dst = base + img * (kN * kN) + 1024 * wave + kVec * lane;
+#pragma unroll
+    for (int i = 0; i < Pieces<IO>::kCount; ++i) {
+        const int e = 1024 * wave + kVec * lane + 64 * kVec * i;
+        cpx q[kVec];
+#pragma unroll
+        for (int c = 0; c < kVec; ++c) q[c] = lds[(e >> 7) * kStride + lds_pad((e & 127) + c)];
+        st_nt(reinterpret_cast<W*>(dst + 64 * kVec * i), Io<IO>::encode4(q));
+    }
+}
+
+// Row r of the image as the length-128 transform slot of its 8 lanes.
+template <bool FWD>
+__device__ __forceinline__ void rows(cpx* lds, int r, int t, const LaneTwiddles<kN>& w) {
+    cpx* row = lds + r * kStride;
+    cpx v[16];
+    wave_lds_sync();
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = row[lds_pad(t + 8 * j)];
+    fft_registers<kN, FWD>(v, row, t, w);
+    wave_lds_sync();
+#pragma unroll
+    for (int j = 0; j < 16; ++j) row[lds_pad(t + 8 * j)] = v[j];
+}
+}  // namespace conv2d128
+
+template <class IO>
+__global__ __launch_bounds__(1024) void conv2d128_kernel(const IO* __restrict__ x,
+                                                         const IO* __restrict__ h,
+                                                         IO* __restrict__ y, int batch,
+                                                         const float2* __restrict__ tw) {
+    using namespace conv2d128;
+    __shared__ cpx lds[kLds];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int t = tid & 7;
+    const int r = 8 * wave + (lane >> 3);  // row of the row phases
+    const int c = tid >> 3;                // column of the column phase
+    const StridedSlot col{lds + lds_pad(c), kStride};
+    LaneTwiddles<kN> w;
+    w.load(t, tw);
+    constexpr int kE = kEarly<IO>, kAll = Pieces<IO>::kCount;
+
+    long long img, img_end, step;
+    tile_walk(batch, 0, img, img_end, step);
+    if (img >= img_end) return;  // uniform over the workgroup
+
+    // The filter's spectrum / 16384 in the column layout: hs[j] = H[t + 8 j][c].
+    Pieces<IO> raw;
+    load<0, kAll>(raw, h, 0, wave, lane);
+    stage(raw, lds, wave, lane);
+    load<0, kAll>(raw, x, img, wave, lane);
+    rows<true>(lds, r, t, w);
+    __syncthreads();
+    cpx hs[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) hs[j] = slot_at(col, t + 8 * j);
+    fft_registers<kN, true>(hs, col, t, w);
+    constexpr float kScale = 1.0f / (kN * kN);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) hs[j] = {hs[j].re * kScale, hs[j].im * kScale};
+    __syncthreads();  // every column read of the filter is done
+
+    for (; img < img_end; img += step) {
+        const bool next = img + step < img_end;
+        wave_lds_sync();
+        stage(raw, lds, wave, lane);
+        if (next) load<0, kE>(raw, x, img + step, wave, lane);
+        rows<true>(lds, r, t, w);
+        __syncthreads();
+        cpx v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = slot_at(col, t + 8 * j);
+        fft_registers<kN, true>(v, col, t, w);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = cmul(v[j], hs[j]);
+        fft_registers<kN, false>(v, col, t, w);
+        wave_lds_sync();
+#pragma unroll
+        for (int j = 0; j < 16; ++j) slot_at(col, t + 8 * j) = v[j];
+        __syncthreads();
+        rows<false>(lds, r, t, w);
+        wave_lds_sync();
+        store(y, img, lds, wave, lane);
+        if (next) load<kE, kAll>(raw, x, img + step, wave, lane);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Column pass of the multi-pass 2-D convolution of images too large for one
+// workgroup (R x C = 1024 x 1024 here; the reference's built 2-D convolution
+// is the same split, sample/conv2d/thunder.cu:70-207: row FFT kernel, a
+// column kernel that runs FFT x H x IFFT, an inverse row kernel).  The row
+// passes are the library's C2C kernels; this kernel does the columns.
+// A workgroup of 512 lanes takes 8 adjacent columns of one image (a unit):
+// it loads the R x 8 block in 16-byte pieces of whole rows (64 bytes per row
+// fp32, 32 half), stages it column by column into LDS slots, and wave w
+// transforms column c0 + w (R / 16 = 64 lanes, 16 values each) in its slot:
+//   kConv:  out = IFFT_col(FFT_col(in) * H[., c0 + w])  (H fp32, R x C)
+//   !kConv: out = scale * FFT_col(in)                   (a filter's spectrum)
+// then stages the results back and stores them the way they came.  In and
+// out may be the same buffer (each unit reads its block before writing it).
+// Units are walked grid-stride; with a grid that is a multiple of the column
+// blocks per image, a workgroup keeps one column block for every image, so
+// its H column is loaded once and held in registers.  Slots are kSlotStride
+// apart (2 kSlotStride = 8 mod 64 banks), so the staging accesses of a
+// half-wave (4 columns x 8 rows) fall on distinct banks.  The next unit's
+// pieces are loaded before the current unit is transformed: held to 2 waves
+// per SIMD (one workgroup per CU), the kernel keeps its block, the next
+// block and the H column in registers without spilling (at 4 per SIMD the
+// forward and inverse column transforms alone spill).
+// ---------------------------------------------------------------------------
+namespace conv2dcols {
+template <int R>
+inline constexpr int kSlotStride = C2CPlan<R>::kSlot + 4;
+
+// Cols columns per unit (one per wave: 64 Cols lanes).
+template <class IO, int R, int Cols>
+struct Block {
+    static constexpr int kVec = Io<IO>::kVec;
+    static constexpr int kPer = Cols / kVec;                 // pieces per row
+    static constexpr int kRowsPerStep = 64 * Cols / kPer;    // rows per lane step
+    static constexpr int kCount = R / kRowsPerStep;     // pieces per lane
+    typename Io<IO>::W4 w[kCount];
+};
+
+template <int First, int Last, int C, class IO, int R, int Cols>
+__device__ __forceinline__ void load(Block<IO, R, Cols>& b, const IO* in, long long base, int tid) {
+    constexpr long long cols = C;
+    using B = Block<IO, R, Cols>;
+    const int p = tid % B::kPer, r0 = tid / B::kPer;
+#pragma unroll
+    for (int i = First; i < Last; ++i) {
+        const long long e = base + static_cast<long long>(r0 + B::kRowsPerStep * i) * cols + B::kVec * p;
+        b.w[i] = ld_nt(reinterpret_cast<const typename Io<IO>::W4*>(in + e));
+    }
+}
+
+template <class IO, int R, int Cols>
+__device__ __forceinline__ void stage(const Block<IO, R, Cols>& b, cpx* lds, int tid) {
+    using B = Block<IO, R, Cols>;
+    const int p = tid % B::kPer, r0 = tid / B::kPer;
+#pragma unroll
+    for (int i = 0; i < B::kCount; ++i) {
+        cpx q[B::kVec];
+        Io<IO>::decode4(b.w[i], q);
+#pragma unroll
+        for (int c = 0; c < B::kVec; ++c)
+            lds[(B::kVec * p + c) * kSlotStride<R> + lds_pad(r0 + B::kRowsPerStep * i)] = q[c];
+    }
+}
+
+template <int C, class IO, int R, int Cols>
+__device__ __forceinline__ void store(IO* out, long long base, const cpx* lds, int tid) {
+    constexpr long long cols = C;
+    using B = Block<IO, R, Cols>;
+    const int p = tid % B::kPer, r0 = tid / B::kPer;
+#pragma unroll
+    for (int i = 0; i < B::kCount; ++i) {
+        cpx q[B::kVec];
+#pragma unroll
+        for (int c = 0; c < B::kVec; ++c)
+            q[c] = lds[(B::kVec * p + c) * kSlotStride<R> + lds_pad(r0 + B::kRowsPerStep * i)];
+        const long long e = base + static_cast<long long>(r0 + B::kRowsPerStep * i) * cols + B::kVec * p;
+        st_nt(reinterpret_cast<typename Io<IO>::W4*>(out + e), Io<IO>::encode4(q));
+    }
+}
+}  // namespace conv2dcols
+
+// Waves per SIMD: 8 columns per unit (512 lanes) hold two, with the next
+// unit's block prefetched; 4 columns (256 lanes) three, loading each block
+// when its unit starts (the prefetch would spill there).
+template <int Cols>
+inline constexpr int kColsWavesPerEU = Cols == 8 ? 2 : 3;
+template <int Cols>
+inline constexpr bool kColsPrefetch = Cols == 8;
+
+template <class In, class Out, int R, int C, bool kConv, int Cols>
+__global__ __launch_bounds__(64 * Cols) __attribute__((amdgpu_waves_per_eu(kColsWavesPerEU<Cols>))) void
+conv2d_cols_kernel(const In* in, Out* out, const float2* __restrict__ H, long long units,
+                   float scale, const float2* __restrict__ tw) {
+    using P = C2CPlan<R>;
+    static_assert(P::kTPF == 64, "one wave per column");
+    using namespace conv2dcols;
+    __shared__ __align__(16) cpx lds[Cols * kSlotStride<R>];
+    const int tid = threadIdx.x, wave = tid >> 6, t = tid & 63;
+    LaneTwiddles<R> w;
+    w.load(t, tw);
+    cpx* const slot = lds + wave * kSlotStride<R>;
+    constexpr long long cols = C;
+    constexpr long long blocks_per_image = C / Cols;
+    constexpr int kAll = Block<In, R, Cols>::kCount;
+
+    auto where = [&](long long u, long long& base, int& c0) {
+        const long long img = u / blocks_per_image;
+        c0 = static_cast<int>(u - img * blocks_per_image) * Cols;
+        base = img * R * static_cast<long long>(cols) + c0;
+    };
+    long long u = blockIdx.x;
+    if (u >= units) return;  // uniform over the workgroup
+    long long base;
+    int c0;
+    where(u, base, c0);
+    Block<In, R, Cols> raw;
+    if constexpr (kColsPrefetch<Cols>) load<0, kAll, C>(raw, in, base, tid);
+    int h_c0 = -1;
+    cpx hs[kConv ? 16 : 1];
+    for (; u < units; u += gridDim.x) {
+        const long long next_u = u + gridDim.x;
+        long long next_base = 0;
+        int next_c0 = 0;
+        if (next_u < units) where(next_u, next_base, next_c0);
+        if constexpr (!kColsPrefetch<Cols>) load<0, kAll, C>(raw, in, base, tid);
+        __syncthreads();  // the previous unit's reads of the slots are done
+        stage(raw, lds, tid);
+        if constexpr (kColsPrefetch<Cols>)
+            if (next_u < units) load<0, kAll, C>(raw, in, next_base, tid);
+        if constexpr (kConv) {
+            if (c0 != h_c0) {  // uniform: this workgroup's column block changed
+                const float2* hc = H + c0 + wave;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const float2 hk = hc[static_cast<long long>(t + 64 * j) * cols];
+                    hs[j] = {hk.x, hk.y};
+                }
+                h_c0 = c0;
+            }
+        }
+        __syncthreads();
+        cpx v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = slot[lds_pad(t + 64 * j)];
+        fft_registers<R, true>(v, slot, t, w);
+        if constexpr (kConv) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = cmul(v[j], hs[j]);
+            fft_registers<R, false>(v, slot, t, w);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = {v[j].re * scale, v[j].im * scale};
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int j = 0; j < 16; ++j) slot[lds_pad(t + 64 * j)] = v[j];
+        __syncthreads();
+        store<C, Out, R, Cols>(out, base, lds, tid);
+        base = next_base;
+        c0 = next_c0;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Real-input, real-output fused convolution with one real filter per channel
 // (the reference's thunder_convN_block_kernel_realin_realout,
 // sample/conv1d/conv1d_fullfft_l4096_thunder.cu:280-331, generalised to all

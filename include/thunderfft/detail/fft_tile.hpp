@@ -53,6 +53,16 @@ struct C2CPlan {
 
 __device__ __forceinline__ int lds_pad(int i) { return i + (i >> 4); }
 
+// A transform's LDS slot: element i of a contiguous slot sits at lds_pad(i);
+// a strided slot holds element i at base[i * stride] (a column of an image
+// kept row-major in LDS, transformed where it lies).
+__device__ __forceinline__ cpx& slot_at(cpx* slot, int i) { return slot[lds_pad(i)]; }
+struct StridedSlot {
+    cpx* base;
+    int stride;
+};
+__device__ __forceinline__ cpx& slot_at(StridedSlot s, int i) { return s.base[i * s.stride]; }
+
 template <bool WaveLocal>
 __device__ __forceinline__ void region_sync() {
     if constexpr (WaveLocal)
@@ -145,8 +155,8 @@ struct LaneTwiddles {
 
 // One Stockham pass p >= 1: write the previous pass's outputs to LDS, read
 // this pass's inputs, twiddle, DFT.
-template <int N, bool FWD, int R, int L, int RPrev, int LPrev>
-__device__ __forceinline__ void stockham_pass(cpx (&v)[16], cpx* slot, int t,
+template <int N, bool FWD, int R, int L, int RPrev, int LPrev, class Slot>
+__device__ __forceinline__ void stockham_pass(cpx (&v)[16], Slot slot, int t,
                                               const PassTwiddles<N, R, L>& tw) {
     using P = C2CPlan<N>;
     // previous outputs: butterfly b = t + TPF*q, output m -> (b/LPrev)*LPrev*RPrev + b%LPrev + m*LPrev
@@ -156,7 +166,7 @@ __device__ __forceinline__ void stockham_pass(cpx (&v)[16], cpx* slot, int t,
         const int b = t + P::kTPF * q;
         const int base = (b / LPrev) * LPrev * RPrev + (b % LPrev);
 #pragma unroll
-        for (int m = 0; m < RPrev; ++m) slot[lds_pad(base + m * LPrev)] = v[q * RPrev + m];
+        for (int m = 0; m < RPrev; ++m) slot_at(slot, base + m * LPrev) = v[q * RPrev + m];
     }
     region_sync<P::kWaveLocal>();
     cpx w[R - 1];
@@ -164,10 +174,10 @@ __device__ __forceinline__ void stockham_pass(cpx (&v)[16], cpx* slot, int t,
     static_for<0, 16 / R>([&](auto qc) {
         constexpr int q = decltype(qc)::value;
         const int b = t + P::kTPF * q;
-        v[q * R] = slot[lds_pad(b)];
+        v[q * R] = slot_at(slot, b);
         static_for<1, R>([&](auto jc) {
             constexpr int j = decltype(jc)::value;
-            const cpx x = slot[lds_pad(b + j * (N / R))];
+            const cpx x = slot_at(slot, b + j * (N / R));
             v[q * R + j] = rot<16, j * q, FWD>(FWD ? cmulc(x, w[j - 1]) : cmul(x, w[j - 1]));
         });
         Dft<R, FWD>::run(v + q * R);
@@ -175,9 +185,10 @@ __device__ __forceinline__ void stockham_pass(cpx (&v)[16], cpx* slot, int t,
 }
 
 // The whole transform of the lane's transform slot: v[j] = x[t + TPF*j] in,
-// v[j] = X[t + TPF*j] out.  `slot` is the transform's LDS slot.
-template <int N, bool FWD>
-__device__ __forceinline__ void fft_registers(cpx (&v)[16], cpx* slot, int t,
+// v[j] = X[t + TPF*j] out.  `slot` is the transform's LDS slot (cpx* or
+// StridedSlot).
+template <int N, bool FWD, class Slot>
+__device__ __forceinline__ void fft_registers(cpx (&v)[16], Slot slot, int t,
                                               const LaneTwiddles<N>& w) {
     using P = C2CPlan<N>;
     Dft<16, FWD>::run(v);

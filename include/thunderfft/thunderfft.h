@@ -170,11 +170,15 @@ int thff_conv1d_valid_async(int precision, const void* d_x, long long input_len,
  * column IFFT -> row IFFT over one 1024 x 1024 image, and the unbuilt 64 x 64
  * tile sketch sample/conv2d/thunder_tile64.cu:33-208):
  *   y[b][r][c] = sum_{r',c'} x[b][r'][c'] * h[(r - r') mod rows][(c - c') mod cols],
- * computed as IFFT2(FFT2(x[b]) * FFT2(h)) / (rows*cols) in one kernel per
- * image.  rows = cols = 64 (THFF_EINVAL otherwise); requires
- * thff_initialize(precision, 64).  x and y hold batch*rows*cols complex
- * values, h rows*cols.  Same checks, return codes and synchronisation as
- * thff_conv1d. */
+ * computed as IFFT2(FFT2(x[b]) * FFT2(h)) / (rows*cols).  rows = cols = 64 or
+ * 128: one fused kernel (forward 2-D FFT, product, inverse) per image, the
+ * image on chip.  rows = cols = 1024 (the reference's sample shape): the
+ * filter's spectrum goes to a workspace the call allocates stream-ordered
+ * (hipMallocAsync, 8 MiB) and frees the same way, then row FFTs x -> y, a
+ * column pass (FFT, product, inverse FFT) and inverse row FFTs in place in
+ * y.  Other shapes -> THFF_EINVAL; requires thff_initialize(precision, rows).
+ * x and y hold batch*rows*cols complex values, h rows*cols.  Same checks,
+ * return codes and synchronisation as thff_conv1d. */
 int thff_conv2d(int precision, int rows, int cols, const void* d_x, const void* d_h, void* d_y,
                 int batch, void* stream);
 

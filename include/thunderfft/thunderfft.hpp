@@ -150,14 +150,17 @@ inline void ThunderFFT_conv1d_valid(const vec2_t<T>* d_x, long long input_len,
                                     filter_len, d_y, batch, static_cast<void*>(stream)));
 }
 
-// Fused 2-D circular convolution of `batch` Rows x Cols images with one shared
-// filter: y[b] = IFFT2(FFT2(x[b]) * FFT2(h)) / (Rows*Cols).  Rows = Cols = 64;
-// Initialize<T>(64) first.  No counterpart in the reference's library API
-// (its 2-D convolution is sample/conv2d/thunder.cu).
+// 2-D circular convolution of `batch` Rows x Cols images with one shared
+// filter: y[b] = IFFT2(FFT2(x[b]) * FFT2(h)) / (Rows*Cols).  Rows = Cols = 64
+// or 128 (one fused kernel per image), or 1024 (the reference's built sample
+// shape: row pass, fused column pass, inverse row pass); Initialize<T>(Rows)
+// first.  No counterpart in the reference's library API (its 2-D convolution
+// is sample/conv2d/thunder.cu).
 template <typename T, int Rows, int Cols>
 inline void ThunderFFT_conv2d(const vec2_t<T>* d_x, const vec2_t<T>* d_h, vec2_t<T>* d_y, int batch,
                               hipStream_t stream = 0) {
-    static_assert(Rows == 64 && Cols == 64, "ThunderFFT_conv2d supports 64 x 64 images");
+    static_assert(Rows == Cols && (Rows == 64 || Rows == 128 || Rows == 1024),
+                  "ThunderFFT_conv2d supports 64 x 64, 128 x 128 and 1024 x 1024 images");
     detail::check(thff_conv2d(detail::precision_code<T>(), Rows, Cols, d_x, d_h, d_y, batch,
                               static_cast<void*>(stream)));
 }

@@ -457,6 +457,12 @@ int thff_circconv1d_f64(int n, long batch, int per_signal_filter, const double* 
     return 0;
 }
 
+/* Direct 2-D circular convolution, y[r][c] = sum_{dr,dc} h[dr][dc] *
+ * x[(r - dr) mod rows][(c - dc) mod cols], accumulated one filter tap at a
+ * time so that zero taps cost nothing: O(rows cols nnz(h)) per image, which
+ * keeps a 1024 x 1024 image with a 7 x 7 filter (the reference sample's
+ * shape, sample/conv2d/thunder.cu:556-565, with its small f x f filters)
+ * within a second. */
 int thff_circconv2d_f64(int rows, int cols, long batch, const double* x, const double* h,
                         double* y) {
     if (rows <= 0 || cols <= 0 || batch < 0) return -1;
@@ -464,23 +470,25 @@ int thff_circconv2d_f64(int rows, int cols, long batch, const double* x, const d
     for (long b = 0; b < batch; ++b) {
         const double* xs = x + 2 * img * b;
         double* ys = y + 2 * img * b;
-        for (int r = 0; r < rows; ++r)
-            for (int c = 0; c < cols; ++c) {
-                double sr = 0, si = 0;
-                for (int r2 = 0; r2 < rows; ++r2) {
-                    int dr = r - r2;
-                    if (dr < 0) dr += rows;
-                    for (int c2 = 0; c2 < cols; ++c2) {
-                        int dc = c - c2;
-                        if (dc < 0) dc += cols;
-                        const double* a = xs + 2 * ((size_t)r2 * cols + c2);
-                        const double* w = h + 2 * ((size_t)dr * cols + dc);
-                        sr += a[0] * w[0] - a[1] * w[1];
-                        si += a[0] * w[1] + a[1] * w[0];
+        memset(ys, 0, 2 * img * sizeof(double));
+        for (int dr = 0; dr < rows; ++dr)
+            for (int dc = 0; dc < cols; ++dc) {
+                const double wr = h[2 * ((size_t)dr * cols + dc)];
+                const double wi = h[2 * ((size_t)dr * cols + dc) + 1];
+                if (wr == 0.0 && wi == 0.0) continue;
+                for (int r = 0; r < rows; ++r) {
+                    int r2 = r - dr;
+                    if (r2 < 0) r2 += rows;
+                    const double* xrow = xs + 2 * (size_t)r2 * cols;
+                    double* yrow = ys + 2 * (size_t)r * cols;
+                    for (int c = 0; c < cols; ++c) {
+                        int c2 = c - dc;
+                        if (c2 < 0) c2 += cols;
+                        const double ar = xrow[2 * c2], ai = xrow[2 * c2 + 1];
+                        yrow[2 * c] += ar * wr - ai * wi;
+                        yrow[2 * c + 1] += ar * wi + ai * wr;
                     }
                 }
-                ys[2 * ((size_t)r * cols + c)] = sr;
-                ys[2 * ((size_t)r * cols + c) + 1] = si;
             }
     }
     return 0;

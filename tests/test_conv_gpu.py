@@ -336,6 +336,92 @@ def test_config5_conv2d_64x64(T):
     torch.cuda.empty_cache()
 
 
+def _corner_filter(size, seed, k=7, full=False):
+    """size x size filter: a k x k corner block of i.i.d. N(0, 1/k) real taps
+    (the benchmarked filter's shape), or every tap complex N(0, 1/size^2)."""
+    rng = np.random.default_rng(seed)
+    h = np.zeros((size, size), dtype=np.complex64)
+    if full:
+        s = 1.0 / size
+        h[:] = rng.normal(0, s, (size, size)) + 1j * rng.normal(0, s, (size, size))
+    else:
+        h[:k, :k] = rng.normal(0.0, 1.0 / k, (k, k))
+    return h
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("size", [128, 1024])
+def test_conv2d_large_images_match_direct_convolution(T, size):
+    """128 x 128 (one fused kernel per image) and 1024 x 1024 (the reference
+    sample's shape, sample/conv2d/thunder.cu:556-565: row pass, fused column
+    pass, inverse row pass) against the fp64 direct circular convolution:
+    the 7 x 7 corner filter on 1 and 3 images, a filter with one tap at
+    (dr, dc) (every image rolls by it) and, at 128, a dense complex filter."""
+    import thunderfft_amd as thff
+
+    thff.ThunderFFTInitialize(T, size)
+    cases = [(1, _corner_filter(size, 3)), (3, _corner_filter(size, 4))]
+    imp = np.zeros((size, size), dtype=np.complex64)
+    imp[size // 2 + 3, size - 5] = 1
+    cases.append((2, imp))
+    if size == 128:
+        cases.append((2, _corner_filter(size, 5, full=True)))
+    for batch, h in cases:
+        x = oracle.uniform(size * size, batch, seed=91 + batch + size).reshape(batch, size, size)
+        xr, hr = oracle.represent(x, T), oracle.represent(h, T)
+        d_x, d_h = to_device(xr, T), to_device(hr, T)
+        d_y = to_device(np.full((batch, size, size), np.nan, dtype=np.complex64), T)
+        thff.ThunderFFT_conv2d(T, size, size, d_x, d_h, d_y, batch)
+        y = from_device(d_y, T).reshape(batch, size, size)
+        m = oracle.metrics(y, oracle.circconv2d(xr, hr))
+        nnz = int(np.count_nonzero(h))
+        label = f"{T} conv2d {size}x{size} batch={batch} taps={nnz}: rel_l2={m['rel_l2']:.3e}"
+        print(label, flush=True)
+        assert m["nonfinite"] == 0, label
+        assert m["rel_l2"] <= GATE and m["rel_l2"] <= TIGHT[T], label
+
+
+@pytest.mark.parametrize("T", ["float", "half"])
+@pytest.mark.parametrize("size,batch", [(128, 2048 + 3), (1024, 32)])
+def test_conv2d_large_image_batches(T, size, batch):
+    """Benchmark-sized batches (2^25 values, plus a few images so the walk is
+    uneven at 128): a subset of images against the direct convolution with the
+    7 x 7 corner filter, then a one-tap filter rolls every image."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    img = size * size
+    seed = oracle.BENCH_SEED_BASE + img
+    dt = torch.float32 if T == "float" else torch.float16
+    x = torch.empty(2 * img * batch, dtype=dt, device="cuda")
+    thff.fill_uniform(T, x, img * batch, seed)
+    y = torch.empty_like(x)
+    thff.ThunderFFTInitialize(T, size)
+    h = _corner_filter(size, 6)
+    thff.ThunderFFT_conv2d(T, size, size, x, to_device(h, T), y, batch)
+    rows = np.unique(np.array([0, 1, batch // 2, batch - 2, batch - 1]))
+    sub = from_device(y.view(batch, 2 * img)[torch.from_numpy(rows).cuda()].contiguous(), T)
+    xin = np.concatenate([oracle.uniform(img, 1, seed, first_element=int(r) * img)
+                          for r in rows]).reshape(len(rows), size, size)
+    xin = oracle.represent(xin, T)
+    m = oracle.metrics(sub.reshape(len(rows), size, size),
+                       oracle.circconv2d(xin, oracle.represent(h, T)))
+    print(f"{T} conv2d {size}x{size} batch={batch} subset rel_l2={m['rel_l2']:.3e}", flush=True)
+    assert m["nonfinite"] == 0 and m["rel_l2"] <= GATE and m["rel_l2"] <= TIGHT[T]
+    dr, dc = 7, size - 3
+    imp = np.zeros((size, size), dtype=np.complex64)
+    imp[dr, dc] = 1
+    thff.ThunderFFT_conv2d(T, size, size, x, to_device(imp, T), y, batch)
+    want = torch.roll(x.view(batch, size, size, 2).float(), shifts=(dr, dc), dims=(1, 2))
+    err = float(torch.linalg.vector_norm(y.view(batch, size, size, 2).float() - want) /
+                torch.linalg.vector_norm(want))
+    print(f"  impulse roll over all images rel_l2={err:.3e}", flush=True)
+    assert np.isfinite(err) and err <= TIGHT[T]
+    del x, y
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("T", ["float", "half"])
 def test_conv2d_beyond_2e31_values(T):
     """2^19 + 3 images of 64 x 64 (2^31 + 12288 complex values: 17 GB fp32,

@@ -90,15 +90,22 @@ def test_conv1d_argument_checks():
 
 
 def test_conv2d_argument_checks():
-    """thff_conv2d: 64 x 64 only; the rest as thff_conv1d, before any HIP call."""
-    with pytest.raises(ValueError, match="64 x 64"):
-        thff.ThunderFFT_conv2d("float", 32, 64, 8, 16, 24, 1)
-    with pytest.raises(ValueError, match="nonnegative"):
-        thff.ThunderFFT_conv2d("float", 64, 64, 8, 16, 24, -1)
-    thff.ThunderFFT_conv2d("float", 64, 64, 0, 0, 0, 0)  # zero batch: no-op
-    for args in ((0, 16, 24), (8, 0, 24), (8, 16, 0), (8, 16, 8), (8, 16, 16)):
-        with pytest.raises(ValueError):
-            thff.ThunderFFT_conv2d("float", 64, 64, *args, 1)
+    """thff_conv2d: square 64, 128 or 1024 images only; the rest as
+    thff_conv1d, before any HIP call (the 1024 x 1024 form allocates its
+    workspace only after every check)."""
+    for rows, cols in ((32, 64), (64, 128), (128, 64), (256, 256), (2048, 2048), (1024, 512)):
+        with pytest.raises(ValueError, match="64 x 64, 128 x 128 and 1024 x 1024"):
+            thff.ThunderFFT_conv2d("float", rows, cols, 16, 32, 48, 1)
+    for size in (64, 128, 1024):
+        with pytest.raises(ValueError, match="nonnegative"):
+            thff.ThunderFFT_conv2d("float", size, size, 16, 32, 48, -1)
+        thff.ThunderFFT_conv2d("half", size, size, 0, 0, 0, 0)  # zero batch: no-op
+        for args in ((0, 16, 32), (16, 0, 32), (16, 32, 0), (16, 32, 16), (16, 32, 32),
+                     (24, 32, 48), (16, 40, 48), (16, 32, 56)):
+            with pytest.raises(ValueError):
+                thff.ThunderFFT_conv2d("float", size, size, *args, 1)
+    with pytest.raises(ValueError, match="exceeds one launch"):
+        thff.ThunderFFT_conv2d("float", 1024, 1024, 16, 32, 48, (1 << 16) + 1)
 
 
 def test_conv1d_real_argument_checks():

@@ -208,6 +208,23 @@ def test_circconv_matches_fft_product():
     assert rel(oracle.circconv2d(x2, h2), expect2) < 1e-13
 
 
+def test_circconv2d_sparse_filters_pinned():
+    """The 2-D oracle skips zero taps: a single complex tap at (dr, dc) gives
+    w * roll(x, (dr, dc)) (a transposed or correlated form fails), a sparse
+    corner block on non-square images matches numpy's FFT product, and an
+    all-zero filter gives zeros."""
+    rng = np.random.default_rng(29)
+    x = rng.standard_normal((2, 48, 40)) + 1j * rng.standard_normal((2, 48, 40))
+    h = np.zeros((48, 40), dtype=np.complex128)
+    h[5, 37] = 0.75 - 0.5j
+    assert rel(oracle.circconv2d(x, h), (0.75 - 0.5j) * np.roll(x, (5, 37), axis=(1, 2))) < 1e-15
+    h = np.zeros((48, 40), dtype=np.complex128)
+    h[:7, :3] = rng.standard_normal((7, 3)) + 1j * rng.standard_normal((7, 3))
+    expect = np.fft.ifft2(np.fft.fft2(x) * np.fft.fft2(h))
+    assert rel(oracle.circconv2d(x, h), expect) < 1e-13
+    assert np.array_equal(oracle.circconv2d(x, np.zeros_like(h)), np.zeros_like(x))
+
+
 def test_circconv_channels_pinned():
     """Real per-channel convolution: numpy's FFT product, a shifted impulse
     (y = c * roll(x, k0): a correlation or a wrong channel would fail), the

@@ -209,8 +209,9 @@ def ThunderFFT_conv1d_valid_async(T, d_x, input_len: int, d_taps, filter_len: in
 
 
 def ThunderFFT_conv2d(T, rows: int, cols: int, d_x, d_h, d_y, batch: int, stream=0) -> None:
-    """Fused 2-D circular convolution y[b] = IFFT2(FFT2(x[b]) * FFT2(h)) / (rows*cols);
-    64 x 64 images, one shared filter; synchronous."""
+    """2-D circular convolution y[b] = IFFT2(FFT2(x[b]) * FFT2(h)) / (rows*cols) with
+    one shared filter: 64 x 64 and 128 x 128 images in one fused kernel per image,
+    1024 x 1024 as row pass, fused column pass, inverse row pass; synchronous."""
     _raise(lib().thff_conv2d(_precision(T), int(rows), int(cols), _ptr(d_x), _ptr(d_h), _ptr(d_y),
                              int(batch), _stream(stream)))
 

@@ -411,6 +411,63 @@ hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y,
 }
 #endif
 
+#if THFF_N == 128
+hipError_t launch_conv2d128(int precision, const void* x, const void* h, void* y, int batch,
+                            const float2* tw, int num_cus, hipStream_t stream) {
+    // One image per workgroup of 1024 lanes; the image's 140 KiB of LDS
+    // allow one per CU, so a device grid of one per CU walks the images.
+    const Grid g = make_grid(batch, 1, num_cus);
+    if (precision == 0)
+        conv2d128_kernel<float2><<<g.blocks, 1024, 0, stream>>>(
+            static_cast<const float2*>(x), static_cast<const float2*>(h), static_cast<float2*>(y),
+            batch, tw);
+    else
+        conv2d128_kernel<__half2><<<g.blocks, 1024, 0, stream>>>(
+            static_cast<const __half2*>(x), static_cast<const __half2*>(h),
+            static_cast<__half2*>(y), batch, tw);
+    return hipGetLastError();
+}
+#endif
+
+#if THFF_N == 1024
+hipError_t launch_conv2d_cols(int precision, bool conv, const void* in, void* out,
+                              const float2* H, int cols, long long images, float scale,
+                              const float2* tw, int num_cus, hipStream_t stream) {
+    if (cols != 1024) return hipErrorInvalidValue;  // the kernels are built for 1024 columns
+    // kCols columns per unit, one wave per column; workgroups walk the units
+    // grid-stride, and the grid is a multiple of the image's column blocks, so
+    // every workgroup keeps one column block (and its H column).  Measured on
+    // MI355X, 32 images of 1024 x 1024 end to end: 8 columns (64-byte row
+    // pieces fp32, one 512-lane workgroup per CU with the next block
+    // prefetched) 419 us fp32 / 394 us half, against 790 / 662 us with 4
+    // columns (32-byte pieces, three 256-lane workgroups per CU).
+    constexpr int kCols = 8;
+    constexpr int kPerCu = kColsWavesPerEU<kCols> * 4 / kCols;
+    const long long blocks_per_image = cols / kCols;
+    const long long units = blocks_per_image * images;
+    long long grid = static_cast<long long>(kPerCu) * (num_cus > 0 ? num_cus : 256);
+    if (grid >= blocks_per_image) grid -= grid % blocks_per_image;
+    const dim3 blocks(static_cast<unsigned>(units < grid ? units : grid));
+    const dim3 lanes(64 * kCols);
+    if (precision == 0) {
+        if (conv)
+            conv2d_cols_kernel<float2, float2, 1024, 1024, true, kCols><<<blocks, lanes, 0, stream>>>(
+                static_cast<const float2*>(in), static_cast<float2*>(out), H, units, scale, tw);
+        else
+            conv2d_cols_kernel<float2, float2, 1024, 1024, false, kCols><<<blocks, lanes, 0, stream>>>(
+                static_cast<const float2*>(in), static_cast<float2*>(out), H, units, scale, tw);
+    } else {
+        if (conv)
+            conv2d_cols_kernel<__half2, __half2, 1024, 1024, true, kCols><<<blocks, lanes, 0, stream>>>(
+                static_cast<const __half2*>(in), static_cast<__half2*>(out), H, units, scale, tw);
+        else
+            conv2d_cols_kernel<__half2, float2, 1024, 1024, false, kCols><<<blocks, lanes, 0, stream>>>(
+                static_cast<const __half2*>(in), static_cast<float2*>(out), H, units, scale, tw);
+    }
+    return hipGetLastError();
+}
+#endif
+
 template hipError_t launch_c2c<THFF_N>(int, bool, bool, const void*, void*, int, const float2*,
                                        int, hipStream_t);
 template hipError_t launch_conv1d<THFF_N>(int, bool, const void*, const void*, void*, int,

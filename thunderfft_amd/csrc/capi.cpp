@@ -321,12 +321,18 @@ int conv1d_valid_impl(int precision, const void* x, long long input_len, const v
     return finish(s, synchronize, "ThunderFFT_conv1d_valid synchronize");
 }
 
+// 2-D convolution sizes: rows = cols = 64 and 128 run one fused kernel per
+// image (the image stays on chip); 1024 runs the multi-pass form of the
+// reference's built sample (sample/conv2d/thunder.cu:70-207): the filter's
+// spectrum into a stream-ordered workspace, then row FFTs (the C2C kernel),
+// a column pass doing FFT x H x IFFT, and inverse row FFTs, in place in y.
 int conv2d_impl(int precision, int rows, int cols, const void* x, const void* h, void* y,
                 int batch, void* stream, bool synchronize) {
     if (!supported_precision(precision))
         return fail(THFF_EINVAL, "ThunderFFT_conv2d supports float and half only");
-    if (rows != 64 || cols != 64)
-        return fail(THFF_EINVAL, "ThunderFFT_conv2d supports 64 x 64 images only");
+    if (rows != cols || (rows != 64 && rows != 128 && rows != 1024))
+        return fail(THFF_EINVAL,
+                    "ThunderFFT_conv2d supports 64 x 64, 128 x 128 and 1024 x 1024 images only");
     if (batch < 0) return fail(THFF_EINVAL, "ThunderFFT batch must be nonnegative");
     if (batch == 0) return THFF_OK;
     if (!x || !h || !y)
@@ -335,13 +341,41 @@ int conv2d_impl(int precision, int rows, int cols, const void* x, const void* h,
         return fail(THFF_EINVAL, "ThunderFFT_conv2d output must not alias its inputs");
     if (!aligned16(x) || !aligned16(h) || !aligned16(y))
         return fail(THFF_EINVAL, "ThunderFFT_conv2d requires 16-byte aligned buffers");
-    if (batch > (1 << 24)) return fail(THFF_EINVAL, "ThunderFFT batch exceeds one launch");
+    if (batch > (rows == 1024 ? (1 << 16) : (1 << 24)))
+        return fail(THFF_EINVAL, "ThunderFFT batch exceeds one launch");
     const float2* table = nullptr;
     int cus = 0;
-    const int rc = cached_table(precision, 64, "ThunderFFT_conv2d", &table, &cus);
+    const int rc = cached_table(precision, rows, "ThunderFFT_conv2d", &table, &cus);
     if (rc != THFF_OK) return rc;
     auto s = static_cast<hipStream_t>(stream);
-    hipError_t err = thff::launch_conv2d64(precision, x, h, y, batch, table, cus, s);
+    hipError_t err = hipSuccess;
+    if (rows == 64) {
+        err = thff::launch_conv2d64(precision, x, h, y, batch, table, cus, s);
+    } else if (rows == 128) {
+        err = thff::launch_conv2d128(precision, x, h, y, batch, table, cus, s);
+    } else {
+        constexpr int kN = 1024;
+        const size_t spectrum_bytes = sizeof(float2) * kN * kN;
+        void* spectrum = nullptr;
+        err = hipMallocAsync(&spectrum, spectrum_bytes, s);
+        if (err != hipSuccess) return fail_hip(err, "ThunderFFT_conv2d workspace");
+        auto* H = static_cast<float2*>(spectrum);
+        const int row_signals = batch * kN;
+        // H = FFT2(h) / (rows * cols): columns (scaled, into fp32), then rows in place
+        err = thff::launch_conv2d_cols(precision, false, h, H, nullptr, kN, 1,
+                                       1.0f / (static_cast<float>(kN) * kN), table, cus, s);
+        if (err == hipSuccess)
+            err = thff::launch_c2c<kN>(THFF_FLOAT, true, true, H, H, kN, table, cus, s);
+        if (err == hipSuccess)
+            err = thff::launch_c2c<kN>(precision, true, true, x, y, row_signals, table, cus, s);
+        if (err == hipSuccess)
+            err = thff::launch_conv2d_cols(precision, true, y, y, H, kN, batch, 0.0f, table,
+                                           cus, s);
+        if (err == hipSuccess)
+            err = thff::launch_c2c<kN>(precision, false, true, y, y, row_signals, table, cus, s);
+        const hipError_t ferr = hipFreeAsync(spectrum, s);
+        if (err == hipSuccess) err = ferr;
+    }
     if (err != hipSuccess) return fail_hip(err, "ThunderFFT_conv2d launch");
     if (synchronize) {
         err = hipStreamSynchronize(s);

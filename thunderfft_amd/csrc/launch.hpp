@@ -46,7 +46,21 @@ hipError_t launch_conv1d_valid(int precision, const void* x, long long len, cons
 hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y, int batch,
                            const float2* tw, int num_cus, hipStream_t stream);
 
-// Transforms per tile (4096 complex values, one workgroup pass) for length N.
+// Enqueue the fused 2-D circular convolution of `batch` 128 x 128 images with
+// one shared 128 x 128 filter h (tw: the N = 128 table).
+hipError_t launch_conv2d128(int precision, const void* x, const void* h, void* y, int batch,
+                            const float2* tw, int num_cus, hipStream_t stream);
+
+// Enqueue the column pass of the multi-pass 2-D convolution over `images`
+// 1024-row images with `cols` columns (tw: the N = 1024 table).  conv:
+// out = IFFT_col(FFT_col(in) * H) (in, out: the precision's storage, may be
+// the same buffer; H fp32 rows x cols); otherwise out = scale * FFT_col(in)
+// with out fp32 complex.
+hipError_t launch_conv2d_cols(int precision, bool conv, const void* in, void* out,
+                              const float2* H, int cols, long long images, float scale,
+                              const float2* tw, int num_cus, hipStream_t stream);
+
+// Transforms per tile (4096 complex values, one workgroup pass) for length N.// Transforms per tile (4096 complex values, one workgroup pass) for length N.
 int c2c_transforms_per_block(int n);
 
 
