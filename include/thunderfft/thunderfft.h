@@ -186,6 +186,20 @@ int thff_conv2d(int precision, int rows, int cols, const void* d_x, const void* 
 int thff_conv2d_async(int precision, int rows, int cols, const void* d_x, const void* d_h,
                       void* d_y, int batch, void* stream);
 
+/* thff_conv2d_async that allocates nothing.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, checks, results and return codes as thff_conv2d_async
+ * (enqueued on `stream`, no synchronisation); the 1024 x 1024 form keeps the
+ * filter's spectrum in a device array of the library (8 MiB per GPU, held
+ * until the process ends) instead of a stream-ordered allocation, so images
+ * larger than 1024 x 1024 are THFF_EINVAL.  Every call on one GPU shares
+ * that array: calls that overlap on one GPU (other streams, other threads)
+ * race and must be serialised by the caller.  Requires
+ * thff_initialize(precision, rows) on the current device, as thff_conv2d. */
+int thff_conv2d_noalloc(int precision, int rows, int cols, const void* d_x, const void* d_h,
+                        void* d_y, int batch, void* stream);
+
 /* Snapshot of the current device's twiddle cache for `precision`: the device
  * pointer (NULL when released) and its length (0 when released).  The
  * reference exposes the same state through its device symbols

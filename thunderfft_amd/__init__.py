@@ -25,7 +25,7 @@ __all__ = [
     "SUPPORTED_N", "PRECISIONS", "lib", "ThunderFFTInitialize", "ThunderFFTFinalize",
     "ThunderFFT_global", "ThunderFFT_global_async", "twiddle_info", "fill_uniform",
     "fft", "transforms_per_block", "LIB_PATH", "ThunderFFT_conv1d", "ThunderFFT_conv1d_async",
-    "ThunderFFT_conv2d", "ThunderFFT_conv2d_async", "copy_nt",
+    "ThunderFFT_conv2d", "ThunderFFT_conv2d_async", "ThunderFFT_conv2d_noalloc", "copy_nt",
 ]
 
 SUPPORTED_N = (64, 128, 256, 512, 1024, 2048, 4096)
@@ -67,6 +67,7 @@ def lib() -> ctypes.CDLL:
         c2sig = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, vp, ctypes.c_int, vp]
         L.thff_conv2d.argtypes = c2sig
         L.thff_conv2d_async.argtypes = c2sig
+        L.thff_conv2d_noalloc.argtypes = c2sig
         rfsig = [ctypes.c_int, ctypes.c_int, vp, vp, ctypes.c_int, ctypes.c_float, vp]
         L.thff_conv1d_real_filter.argtypes = rfsig
         L.thff_conv1d_real_filter_async.argtypes = rfsig
@@ -220,6 +221,15 @@ def ThunderFFT_conv2d_async(T, rows: int, cols: int, d_x, d_h, d_y, batch: int, 
     """As ThunderFFT_conv2d, but returns once the launch is enqueued on ``stream``."""
     _raise(lib().thff_conv2d_async(_precision(T), int(rows), int(cols), _ptr(d_x), _ptr(d_h),
                                    _ptr(d_y), int(batch), _stream(stream)))
+
+
+def ThunderFFT_conv2d_noalloc(T, rows: int, cols: int, d_x, d_h, d_y, batch: int,
+                              stream=0) -> None:
+    """As ThunderFFT_conv2d_async, but allocates no device memory (the 1024 x 1024
+    form keeps its filter spectrum in the library's per-GPU device array; calls
+    that overlap on one GPU race)."""
+    _raise(lib().thff_conv2d_noalloc(_precision(T), int(rows), int(cols), _ptr(d_x), _ptr(d_h),
+                                     _ptr(d_y), int(batch), _stream(stream)))
 
 
 def twiddle_info(T) -> tuple[int, int]:

@@ -63,6 +63,40 @@ struct DeviceTables {
 DeviceTables g_tables[2][kMaxDevices];
 std::mutex g_mutex[2];
 
+// Workspace of the allocation-free 2-D convolution (thff_conv2d_noalloc):
+// one fp32 spectrum of the largest image the multi-pass form takes,
+// 1024 x 1024 (8 MiB), in a device array of this library's code object, so
+// that each GPU the library runs on holds its own copy until the process
+// ends.  In host code `scratch` names the symbol, not a device address: the
+// address of the current device's copy is resolved once per device with
+// hipGetSymbolAddress (in ThunderFFTInitialize, which every convolution
+// requires first, or at the first call) and kept in g_scratch.  Every
+// allocation-free call on a GPU shares that GPU's copy: calls that overlap on
+// one GPU race.  Nothing in it needs clearing: the filter pass writes every
+// value before the column pass reads it.
+constexpr long long kScratchValues = 1024LL * 1024LL;
+__device__ __align__(256) float2 scratch[kScratchValues];
+std::atomic<float2*> g_scratch[kMaxDevices] = {};
+std::mutex g_scratch_mutex;
+
+// This device's copy of `scratch` (device: the current device).
+int scratch_address(int device, float2** out) {
+    float2* p = g_scratch[device].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mutex);
+        p = g_scratch[device].load(std::memory_order_relaxed);
+        if (!p) {
+            void* address = nullptr;
+            const hipError_t err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+            if (err != hipSuccess) return fail_hip(err, "hipGetSymbolAddress (conv2d workspace)");
+            p = static_cast<float2*>(address);
+            g_scratch[device].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return THFF_OK;
+}
+
 int length_slot(int n) {
     int s = 0;
     while ((64 << s) < n) ++s;
@@ -327,7 +361,7 @@ int conv1d_valid_impl(int precision, const void* x, long long input_len, const v
 // spectrum into a stream-ordered workspace, then row FFTs (the C2C kernel),
 // a column pass doing FFT x H x IFFT, and inverse row FFTs, in place in y.
 int conv2d_impl(int precision, int rows, int cols, const void* x, const void* h, void* y,
-                int batch, void* stream, bool synchronize) {
+                int batch, void* stream, bool synchronize, bool allocate = true) {
     if (!supported_precision(precision))
         return fail(THFF_EINVAL, "ThunderFFT_conv2d supports float and half only");
     if (rows != cols || (rows != 64 && rows != 128 && rows != 1024))
@@ -343,6 +377,10 @@ int conv2d_impl(int precision, int rows, int cols, const void* x, const void* h,
         return fail(THFF_EINVAL, "ThunderFFT_conv2d requires 16-byte aligned buffers");
     if (batch > (rows == 1024 ? (1 << 16) : (1 << 24)))
         return fail(THFF_EINVAL, "ThunderFFT batch exceeds one launch");
+    if (!allocate && static_cast<long long>(rows) * cols > kScratchValues)
+        return fail(THFF_EINVAL,
+                    "ThunderFFT_conv2d_noalloc: the image exceeds the allocation-free workspace "
+                    "(one 1024 x 1024 spectrum)");
     const float2* table = nullptr;
     int cus = 0;
     const int rc = cached_table(precision, rows, "ThunderFFT_conv2d", &table, &cus);
@@ -357,8 +395,18 @@ int conv2d_impl(int precision, int rows, int cols, const void* x, const void* h,
         constexpr int kN = 1024;
         const size_t spectrum_bytes = sizeof(float2) * kN * kN;
         void* spectrum = nullptr;
-        err = hipMallocAsync(&spectrum, spectrum_bytes, s);
-        if (err != hipSuccess) return fail_hip(err, "ThunderFFT_conv2d workspace");
+        if (allocate) {
+            err = hipMallocAsync(&spectrum, spectrum_bytes, s);
+            if (err != hipSuccess) return fail_hip(err, "ThunderFFT_conv2d workspace");
+        } else {
+            int device = 0;
+            err = hipGetDevice(&device);
+            if (err != hipSuccess) return fail_hip(err, "hipGetDevice (conv2d)");
+            float2* p = nullptr;
+            const int src = scratch_address(device, &p);
+            if (src != THFF_OK) return src;
+            spectrum = p;
+        }
         auto* H = static_cast<float2*>(spectrum);
         const int row_signals = batch * kN;
         // H = FFT2(h) / (rows * cols): columns (scaled, into fp32), then rows in place
@@ -373,8 +421,10 @@ int conv2d_impl(int precision, int rows, int cols, const void* x, const void* h,
                                            cus, s);
         if (err == hipSuccess)
             err = thff::launch_c2c<kN>(precision, false, true, y, y, row_signals, table, cus, s);
-        const hipError_t ferr = hipFreeAsync(spectrum, s);
-        if (err == hipSuccess) err = ferr;
+        if (allocate) {
+            const hipError_t ferr = hipFreeAsync(spectrum, s);
+            if (err == hipSuccess) err = ferr;
+        }
     }
     if (err != hipSuccess) return fail_hip(err, "ThunderFFT_conv2d launch");
     if (synchronize) {
@@ -441,6 +491,9 @@ int thff_initialize(int precision, int n) {
     int device = 0;
     DeviceTables* d = device_tables(precision, "hipGetDevice (initialize)", &device);
     if (!d) return THFF_EIO;
+    float2* workspace = nullptr;  // the allocation-free conv2d's, resolved once per device
+    const int wrc = scratch_address(device, &workspace);
+    if (wrc != THFF_OK) return wrc;
     if (d->current.load(std::memory_order_relaxed) == n) return THFF_OK;
     std::atomic<float2*>& slot = d->table[length_slot(n)];
     if (!slot.load(std::memory_order_relaxed)) {
@@ -541,6 +594,11 @@ int thff_conv2d(int precision, int rows, int cols, const void* d_x, const void* 
 int thff_conv2d_async(int precision, int rows, int cols, const void* d_x, const void* d_h,
                       void* d_y, int batch, void* stream) {
     return conv2d_impl(precision, rows, cols, d_x, d_h, d_y, batch, stream, false);
+}
+
+int thff_conv2d_noalloc(int precision, int rows, int cols, const void* d_x, const void* d_h,
+                        void* d_y, int batch, void* stream) {
+    return conv2d_impl(precision, rows, cols, d_x, d_h, d_y, batch, stream, false, false);
 }
 
 int thff_twiddle_info(int precision, const void** d_table, int* n) {
