@@ -421,7 +421,42 @@ __device__ __forceinline__ unsigned swap_lane_pair(unsigned v) {
         __builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xB1, 0xF, 0xF, false));
 }
 
-template <int N>
+// Buffer addressing of the tile's two rows for kBufferIO: one resource per
+// tile starts at row (2p, d) and spans through row (2p + 1, d), channels * N
+// values further, or covers row 0 alone when the batch is odd and row 1 does
+// not exist.  Every lane then issues the same unconditional 16-byte access:
+// even lanes at their row-0 offset, odd lanes at channels * N values further,
+// and the hardware's range check returns zeros for (and drops the stores of)
+// the missing row.  Byte offsets are 32-bit: the form is used while
+// (channels + 1) * N * 2 bytes fit in 31 bits.
+struct RealRowPair {
+    long long row0;  // element offset of row (2p, d)
+    int bytes;       // resource size: both rows, or row 0 alone
+    __host__ __device__ static RealRowPair at(long long p, int d, int channels, int batch,
+                                              int n) {
+        const long long row0 = (2 * p * channels + d) * static_cast<long long>(n);
+        const int values = 2 * p + 1 < batch ? (channels + 1) * n : n;
+        return {row0, 2 * values};
+    }
+};
+// Byte offset, from row 0, of load piece e (values 64 w + 4 (n & ~1) + 1024 q
+// + 256 e .. + 7 of row 0 for an even lane, of row 1 for an odd one).
+__host__ __device__ __forceinline__ int real4096_load_offset(int channels, int wave, int n, int q,
+                                                             int e) {
+    const int row = (n & 1) ? channels * 4096 : 0;
+    return 2 * (row + 64 * wave + 4 * (n & ~1) + 1024 * q + 256 * e);
+}
+// Byte offset, from row 0, of store piece i of lane tid (values k .. k + 7 of
+// row 0 for an even lane, k - 4 .. k + 3 of row 1 for an odd one, k = 4 tid +
+// 1024 i).
+__host__ __device__ __forceinline__ int real4096_store_offset(int channels, int tid, int i) {
+    const int k = 4 * tid + 1024 * i;
+    return 2 * ((tid & 1) ? channels * 4096 + k - 4 : k);
+}
+// The largest channel count kBufferIO takes at N = 4096.
+inline constexpr int kReal4096BufferMaxChannels = (0x7fffffff / (2 * 4096)) - 1;
+
+template <int N, bool kBufferIO = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
 conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restrict__ spectrum,
                             __half* __restrict__ y, int batch, int channels,
@@ -508,22 +543,44 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
     };
     // Values 64 w + 4 (n & ~1) + 1024 q + 256 e .. + 7 of row 0 (even lanes)
     // or row 1 (odd lanes).
-    auto load = [&](ChannelPos ps, u32x4 (&raw)[4]) {
-        long long r0, r1;
-        rows(ps, r0, r1);
-        const long long row = odd ? r1 : r0;
+    const int load_off = real4096_load_offset(channels, wave, n, q, 0);
+    // kBufferIO: `live` false gives the resource no bytes, so the loads
+    // return zeros without touching memory; every tile then issues the same
+    // loads with no branch, and the compiler counts them exactly (it waits
+    // for the prefetched pieces, not for the previous tile's stores).
+    auto load = [&](ChannelPos ps, u32x4 (&raw)[4], bool live = true) {
+        if constexpr (kBufferIO) {
+            const RealRowPair rp = RealRowPair::at(ps.p, ps.d, channels, batch, N);
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<__half*>(x + rp.row0), 0, live ? rp.bytes : 0, 0x00020000);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int k = 64 * wave + 4 * (n & ~1) + 1024 * q + 256 * e;
-            raw[e] = row >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + row + k)) : u32x4{};
+            for (int e = 0; e < 4; ++e)
+                raw[e] = __builtin_amdgcn_raw_buffer_load_b128(rs, load_off, 512 * e, 2);
+        } else {
+            long long r0, r1;
+            rows(ps, r0, r1);
+            const long long row = odd ? r1 : r0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int k = 64 * wave + 4 * (n & ~1) + 1024 * q + 256 * e;
+                raw[e] = row >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + row + k)) : u32x4{};
+            }
         }
     };
     u32x4 next[4];
-    if (tile < tile_end) load(pos, next);
+    if constexpr (kBufferIO)
+        load(pos, next, tile < tile_end);
+    else if (tile < tile_end)
+        load(pos, next);
     for (; tile < tile_end; tile += step) {
         const long long p = pos.p, d = pos.d;
         long long row0, row1;
         rows(pos, row0, row1);
+        [[maybe_unused]] __amdgpu_buffer_rsrc_t yrs;
+        if constexpr (kBufferIO) {
+            const RealRowPair rp = RealRowPair::at(pos.p, pos.d, channels, batch, N);
+            yrs = __builtin_amdgcn_make_buffer_rsrc(y + rp.row0, 0, rp.bytes, 0x00020000);
+        }
         pos = walk.advance(pos);
         // ---- stage-1 inputs: values 64 w + 4 n + 1024 q + 256 e .. + 3 of both rows ----
         u32x4 z[4];
@@ -538,7 +595,10 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
             z[e] = u32x4{(a0.x & 0xffffu) | (a1.x << 16), (a0.x >> 16) | (a1.x & 0xffff0000u),
                          (a0.y & 0xffffu) | (a1.y << 16), (a0.y >> 16) | (a1.y & 0xffff0000u)};
         }
-        if (tile + step < tile_end) load(pos, next);
+        if constexpr (kBufferIO)
+            load(pos, next, tile + step < tile_end);
+        else if (tile + step < tile_end)
+            load(pos, next);
         cpx v[4][4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
@@ -609,10 +669,16 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
             // k .. k + 7, the odd lane row 1's k - 4 .. k + 3
             const unsigned g0 = swap_lane_pair(odd ? o0.x : o1.x);
             const unsigned g1 = swap_lane_pair(odd ? o0.y : o1.y);
-            if (!odd)
-                st_nt(reinterpret_cast<u32x4*>(y + row0 + k), u32x4{o0.x, o0.y, g0, g1});
-            else if (row1 >= 0)
-                st_nt(reinterpret_cast<u32x4*>(y + row1 + k - 4), u32x4{g0, g1, o1.x, o1.y});
+            if constexpr (kBufferIO) {
+                const u32x4 w4 = odd ? u32x4{g0, g1, o1.x, o1.y} : u32x4{o0.x, o0.y, g0, g1};
+                __builtin_amdgcn_raw_buffer_store_b128(w4, yrs, real4096_store_offset(channels, tid, i),
+                                                       0, 2);
+            } else {
+                if (!odd)
+                    st_nt(reinterpret_cast<u32x4*>(y + row0 + k), u32x4{o0.x, o0.y, g0, g1});
+                else if (row1 >= 0)
+                    st_nt(reinterpret_cast<u32x4*>(y + row1 + k - 4), u32x4{g0, g1, o1.x, o1.y});
+            }
         }
     }
 }

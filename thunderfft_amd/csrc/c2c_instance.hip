@@ -334,9 +334,14 @@ hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectr
     if constexpr (N == 4096) {
         if (precision != 0) {
             const Grid g = make_grid(transforms, 2, num_cus);
-            conv1d_real_mfma4096_kernel<N><<<g.blocks, 256, 0, stream>>>(
-                static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch, channels,
-                tw, g.tiles_per_block);
+            if (channels <= kReal4096BufferMaxChannels)
+                conv1d_real_mfma4096_kernel<N, true><<<g.blocks, 256, 0, stream>>>(
+                    static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch,
+                    channels, tw, g.tiles_per_block);
+            else
+                conv1d_real_mfma4096_kernel<N, false><<<g.blocks, 256, 0, stream>>>(
+                    static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch,
+                    channels, tw, g.tiles_per_block);
             return hipGetLastError();
         }
     }
