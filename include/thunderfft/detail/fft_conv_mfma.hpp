@@ -227,7 +227,9 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
     __shared__ cpx w1[P::kTw1];
     __shared__ u32x4 a3[P::kA3];
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    // The wave index is uniform over the wave: read into a scalar, so that
+    // the per-wave buffer resources below stay in scalar registers.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int n = lane & 15, q = lane >> 4;
     unsigned* region = lds + wave * P::kRegion;
 
@@ -249,13 +251,17 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
         const long long v = (static_cast<long long>(batch) - tl * P::kFPB - wave * P::kFPW) * N;
         return v <= 0 ? 0 : (v >= P::kWaveVals ? P::kWaveVals : static_cast<int>(v));
     };
-    // This wave's kWaveVals values of `src` (nv of them valid), 16-byte loads.
+    // This wave's kWaveVals values of `src` (nv of them valid), 16-byte loads
+    // through a buffer resource of the nv valid values: pieces past them read
+    // zeros by the hardware's range check, so every load is issued with no
+    // branch and the compiler waits for exactly the pieces it uses (with a
+    // guard per piece it waited for every outstanding access, the previous
+    // tile's stores included).  nv = 0 issues loads that touch no memory.
     auto load = [&](const __half2* src, int nv, u32x4 (&raw)[kRaw]) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<__half2*>(src), 0, 4 * nv, 0x00020000);
 #pragma unroll
-        for (int i = 0; i < kRaw; ++i) {
-            const int e = 4 * lane + 256 * i;
-            raw[i] = e < nv ? ld_nt(reinterpret_cast<const u32x4*>(src + e)) : u32x4{};
-        }
+        for (int i = 0; i < kRaw; ++i) raw[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * lane, 1024 * i, 2);
     };
     // Stage loaded values in the wave's region; transform what is staged.
     auto stage = [&](const u32x4 (&raw)[kRaw]) {
@@ -308,11 +314,9 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
     // faster at 2^25 values (at C = 8 the registers are not there).
     constexpr bool kPrefetchShared = !kPerSignal && C <= 4;
     u32x4 rh[kRaw];
-    if constexpr (kPipelined)
-        if (tile < tile_end) load(h + offset(tile), valid(tile), rh);
+    if constexpr (kPipelined) load(h + offset(tile), tile < tile_end ? valid(tile) : 0, rh);
     u32x4 rn[kRaw];
-    if constexpr (kPrefetchShared)
-        if (tile < tile_end) load(x + offset(tile), valid(tile), rn);
+    if constexpr (kPrefetchShared) load(x + offset(tile), tile < tile_end ? valid(tile) : 0, rn);
     // At N = 2048 a wave's issue priority falls as its workgroup gets ahead
     // (ProgressPriority): 63.5 against 66-67 us (shared filter) and 91.0
     // against 91.7-92.0 us (per-signal) at 2^25 values; neutral at N <= 1024.
@@ -340,7 +344,7 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
                 keep(v);
             } else if constexpr (kPrefetchShared) {
                 stage(rn);
-                if (tile + step < tile_end) load(x + offset(tile + step), valid(tile + step), rn);
+                load(x + offset(tile + step), tile + step < tile_end ? valid(tile + step) : 0, rn);
                 forward(v);
             } else {
                 load(x + off, nv, rx);
@@ -358,7 +362,7 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
                 v[b][r] = cmul(v[b][r], cpx{hk.x, hk.y});
             }
         if constexpr (kPipelined)
-            if (tile + step < tile_end) load(h + offset(tile + step), valid(tile + step), rh);
+            load(h + offset(tile + step), tile + step < tile_end ? valid(tile + step) : 0, rh);
         // ---- inverse = conj(DFT(conj(product))) / N, stage 1 from the registers ----
         mfma_stage1_regs<C, true>(a_regs, v);
         mfma_steps2to6<C, true>(region, w1, s3, lane, v);
@@ -374,15 +378,15 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
         // The staging addresses as one base and constant steps: computed per
         // piece, they kept enough registers live to spill one (8 bytes per
         // lane, reloaded among the stores at N = 2048).
-        __half2* dst = y + off;
+        // Stores through a resource of the nv valid values (pieces past them
+        // are dropped by the range check), with no branch.
+        const __amdgpu_buffer_rsrc_t ys =
+            __builtin_amdgcn_make_buffer_rsrc(y + off, 0, 4 * nv, 0x00020000);
         const unsigned* const obase = region + P::out_pad(4 * lane);
 #pragma unroll
-        for (int i = 0; i < kRaw; ++i) {
-            const int e = 4 * lane + 256 * i;
-            if (e < nv)
-                st_nt(reinterpret_cast<u32x4*>(dst + e),
-                      *reinterpret_cast<const u32x4*>(obase + P::kOutStep * i));
-        }
+        for (int i = 0; i < kRaw; ++i)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                *reinterpret_cast<const u32x4*>(obase + P::kOutStep * i), ys, 16 * lane, 1024 * i, 2);
         if constexpr (C == 8) priority.set(--left);
     }
 }
