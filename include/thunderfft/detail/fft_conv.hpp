@@ -768,22 +768,22 @@ struct ChannelWalk {
     long long adv_p;
     int adv_d;
     int channels;
-    __device__ __forceinline__ ChannelWalk(long long adv, int ch) : channels(ch) {
+    __host__ __device__ __forceinline__ ChannelWalk(long long adv, int ch) : channels(ch) {
         adv_p = adv / ch;
         adv_d = static_cast<int>(adv - adv_p * ch);
     }
-    __device__ __forceinline__ ChannelPos at(long long tau) const {
+    __host__ __device__ __forceinline__ ChannelPos at(long long tau) const {
         const long long p = tau / channels;
         return {p, static_cast<int>(tau - p * channels)};
     }
     // (adv_d < channels and q.d < channels: at most one carry)
-    __device__ __forceinline__ ChannelPos advance(ChannelPos q) const {
+    __host__ __device__ __forceinline__ ChannelPos advance(ChannelPos q) const {
         q.p += adv_p;
         q.d += adv_d;
         if (q.d >= channels) q.d -= channels, ++q.p;
         return q;
     }
-    __device__ __forceinline__ void locate(ChannelPos q, int k, long long& pair, int& chan) const {
+    __host__ __device__ __forceinline__ void locate(ChannelPos q, int k, long long& pair, int& chan) const {
         const unsigned s = static_cast<unsigned>(q.d) + static_cast<unsigned>(k);
         const unsigned c = static_cast<unsigned>(channels);
         const unsigned j = s / c;

@@ -60,7 +60,39 @@ __device__ __forceinline__ void split_rows(u32x4 lo, u32x4 hi, u32x4& r0, u32x4&
 template <int C>
 inline constexpr int kConvMfmaMinWavesPerEU = C == 1 || C == 8 ? 2 : 3;
 
+// kBufferIO addressing of conv1d_real_mfma_kernel.  A wave's transforms tau0
+// ... tau0 + kFPW - 1 (pairs p, channels d, consecutive in tau) read and
+// write rows (2p, d) and (2p + 1, d); one resource per wave and tile starts
+// at row 0 of tau0 and runs to the end of the [batch][channels][N] array.
+// Rows are laid out in increasing (p, d) order, so every row of those
+// transforms lies at or after that start, and a row that does not exist --
+// row 1 of the last pair of an odd batch, or any row of a transform past the
+// last -- lies past the end of the array, where the range check reads zeros
+// and drops stores.  Byte offsets from the start stay below
+// (2 channels + 2 kFPW) N * 2, which kBufferIO requires to fit in 31 bits.
+__host__ __device__ __forceinline__ long long real_row(long long p, int d, int r, int channels,
+                                                       int n) {
+    return ((2 * p + r) * static_cast<long long>(channels) + d) * n;
+}
+struct RealWaveSpan {
+    long long start;  // element offset of row 0 of the wave's first transform
+    int bytes;        // from there to the end of the array (0 when past it)
+    __host__ __device__ static RealWaveSpan at(ChannelPos first, int channels, int batch, int n) {
+        const long long start = real_row(first.p, first.d, 0, channels, n);
+        const long long total = static_cast<long long>(batch) * channels * n;
+        const long long left = total > start ? total - start : 0;
+        const long long cap = 0x7ffffff0LL / 2;
+        return {start, static_cast<int>(2 * (left < cap ? left : cap))};
+    }
+};
 template <int C>
+inline constexpr int kRealWaveTransforms = 4 / C > 1 ? 4 / C : 1;
+template <int C>
+__host__ __device__ __forceinline__ bool real_buffer_fits(int channels) {
+    return (2LL * channels + 2 * kRealWaveTransforms<C>) * (256LL * C) * 2 < 0x7ffffff0LL;
+}
+
+template <int C, bool kBufferIO = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kConvMfmaMinWavesPerEU<C>))) void
 conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__ spectrum,
                         __half* __restrict__ y, int batch, int channels,
@@ -74,7 +106,8 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
     __shared__ cpx w1[P::kTw1];
     __shared__ u32x4 a3[P::kA3];
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    // uniform over the wave: a scalar, so the per-wave resources stay scalar
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int n = lane & 15, q = lane >> 4;
     unsigned* region = lds + wave * P::kRegion;
 
@@ -122,12 +155,38 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
             long long p;
             walk.locate(pos, f, p, chan[f]);
         }
+        // kBufferIO: byte offsets of both rows from the wave's resource start,
+        // whether the rows exist or not (see RealWaveSpan).
+        [[maybe_unused]] int off0[kSteps], off1[kSteps];
+        [[maybe_unused]] RealWaveSpan span;
+        if constexpr (kBufferIO) {
+            span = RealWaveSpan::at(pos, channels, batch, N);
+#pragma unroll
+            for (int i = 0; i < kSteps; ++i) {
+                const int e = 8 * lane + 512 * i;
+                long long p;
+                int d;
+                walk.locate(pos, e / N, p, d);
+                off0[i] = static_cast<int>(2 * (real_row(p, d, 0, channels, N) + e % N - span.start));
+                off1[i] = static_cast<int>(2 * (real_row(p, d, 1, channels, N) + e % N - span.start));
+            }
+        }
         pos = walk.advance(pos);
         u32x4 r0[kSteps], r1[kSteps];
+        if constexpr (kBufferIO) {
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<__half*>(x + span.start), 0, span.bytes, 0x00020000);
 #pragma unroll
-        for (int i = 0; i < kSteps; ++i) {
-            r0[i] = base0[i] >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + base0[i])) : u32x4{};
-            r1[i] = base1[i] >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + base1[i])) : u32x4{};
+            for (int i = 0; i < kSteps; ++i) {
+                r0[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off0[i], 0, 2);
+                r1[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off1[i], 0, 2);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kSteps; ++i) {
+                r0[i] = base0[i] >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + base0[i])) : u32x4{};
+                r1[i] = base1[i] >= 0 ? ld_nt(reinterpret_cast<const u32x4*>(x + base1[i])) : u32x4{};
+            }
         }
         wave_lds_sync();  // the previous tile's output reads are done
 #pragma unroll
@@ -190,6 +249,9 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
                 region[P::out_pad((b / C) * N + n + 16 * (b % C) + P::kM * (q + 4 * r))] =
                     pack_half2({v[b][r].re, -v[b][r].im});
         wave_lds_sync();
+        [[maybe_unused]] __amdgpu_buffer_rsrc_t ys;
+        if constexpr (kBufferIO)
+            ys = __builtin_amdgcn_make_buffer_rsrc(y + span.start, 0, span.bytes, 0x00020000);
 #pragma unroll
         for (int i = 0; i < kSteps; ++i) {
             const int e = 8 * lane + 512 * i;
@@ -197,8 +259,13 @@ conv1d_real_mfma_kernel(const __half* __restrict__ x, const float2* __restrict__
             const u32x4 hi = *reinterpret_cast<const u32x4*>(region + P::out_pad(e + 4));
             u32x4 o0, o1;
             split_rows(lo, hi, o0, o1);
-            if (base0[i] >= 0) st_nt(reinterpret_cast<u32x4*>(y + base0[i]), o0);
-            if (base1[i] >= 0) st_nt(reinterpret_cast<u32x4*>(y + base1[i]), o1);
+            if constexpr (kBufferIO) {
+                __builtin_amdgcn_raw_buffer_store_b128(o0, ys, off0[i], 0, 2);
+                __builtin_amdgcn_raw_buffer_store_b128(o1, ys, off1[i], 0, 2);
+            } else {
+                if (base0[i] >= 0) st_nt(reinterpret_cast<u32x4*>(y + base0[i]), o0);
+                if (base1[i] >= 0) st_nt(reinterpret_cast<u32x4*>(y + base1[i]), o1);
+            }
         }
     }
 }

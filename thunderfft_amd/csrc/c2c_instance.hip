@@ -322,9 +322,14 @@ hipError_t launch_conv1d_real(int precision, const void* x, const float2* spectr
             using M = MfmaPlan<N / 256>;
             const long long ntiles = (transforms + M::kFPB - 1) / M::kFPB;
             const Grid g = make_grid(ntiles, N == 256 || N == 2048 ? 2 : 3, num_cus);
-            conv1d_real_mfma_kernel<N / 256><<<g.blocks, 256, 0, stream>>>(
-                static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch, channels,
-                tw, g.tiles_per_block);
+            if (real_buffer_fits<N / 256>(channels))
+                conv1d_real_mfma_kernel<N / 256, true><<<g.blocks, 256, 0, stream>>>(
+                    static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch,
+                    channels, tw, g.tiles_per_block);
+            else
+                conv1d_real_mfma_kernel<N / 256, false><<<g.blocks, 256, 0, stream>>>(
+                    static_cast<const __half*>(x), spectrum, static_cast<__half*>(y), batch,
+                    channels, tw, g.tiles_per_block);
             return hipGetLastError();
         }
     }
