@@ -405,8 +405,8 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
                 keep(v);
             } else if constexpr (kPerSignal) {
                 load(h + off, nv, rh);
-                stage(rh);
                 load(x + off, nv, rx);
+                stage(rh);
                 forward(v);
                 keep(v);
             } else if constexpr (kPrefetchShared) {
@@ -639,9 +639,21 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
         }
     };
     u32x4 next[4];
-    if constexpr (kBufferIO)
-        load(pos, next, tile < tile_end);
-    else if (tile < tile_end)
+    if constexpr (kBufferIO) {
+        if (tile >= tile_end) return;  // uniform over the workgroup
+        load(pos, next);
+        // Four stores to a resource of no bytes (dropped by the range check):
+        // the loop is then entered, like every later pass, with the pieces
+        // followed by four stores in flight, so the compiler's count at the
+        // loop top waits for the pieces only, not for the last tile's stores.
+        // (The size is written as a run-time value, batch >= 0 always, which
+        // keeps the compiler from deleting stores it can prove are dropped.)
+        const __amdgpu_buffer_rsrc_t none =
+            __builtin_amdgcn_make_buffer_rsrc(y, 0, batch < 0 ? 16 : 0, 0x00020000);
+        __builtin_amdgcn_sched_barrier(0);  // after the loads, as in the loop
+#pragma unroll
+        for (int i = 0; i < 4; ++i) __builtin_amdgcn_raw_buffer_store_b128(u32x4{}, none, 16 * i, 0, 2);
+    } else if (tile < tile_end)
         load(pos, next);
     for (; tile < tile_end; tile += step) {
         const long long p = pos.p, d = pos.d;
@@ -698,6 +710,10 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
                     const float2 hk = hs[b + 1024 * r];
                     spec[b][r] = cpx{hk.x, hk.y};
                 }
+            // Wait here, on this rarely taken path: a wait after the branch
+            // would have to count these loads as the latest ones and so
+            // would also wait for the next tile's pieces on every tile.
+            wait_vmem_all();
             spec_d = d;
         }
 #pragma unroll

@@ -227,4 +227,11 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima, gfx9
+// encoding): every vector memory access of the wave has completed.  Placed
+// inside a rarely taken branch that loads, it keeps the compiler from
+// waiting for everything at the branch's join on every pass: after the join
+// it counts only the accesses the common path issued.
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 }  // namespace thff
