@@ -1407,3 +1407,220 @@ conv2d64_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ 
 }
 
 }  // namespace thff
+
+namespace thff {
+
+// ---------------------------------------------------------------------------
+// half2 2-D convolution of 128 x 128 images on MFMA (the contract of
+// conv2d128_kernel: y = IFFT2(FFT2(x) * FFT2(h)) / 16384, one shared filter;
+// the reference's 128-tile sketch is sample/conv2d/thunder_tile128.cu:64-237),
+// one image per workgroup tile of 512 lanes (8 waves).  Both 128-point
+// transforms split as 128 = 16 x 8: a DFT16 on v_mfma_f32_16x16x32_f16 over
+// the stride-8 index with the twiddle W128^(j k) folded into block j's
+// operands, then an in-lane DFT8 over the block index.  Lane (n, q) (lane =
+// n + 16 q) of wave w:
+//   F1 columns: wave w owns the columns c = 16 w + n; block b = r0 holds the
+//      inputs r1 = 4 q + e (row r = r0 + 8 r1) of the staged image; grouped
+//      outputs kr1 = 4 q + t, so after the DFT8 over r0 the lane holds
+//      Xc[kr = 4 q + t + 16 kr0][c]: four consecutive rows per kr0, written
+//      to the exchange buffer as one 16-byte chunk.
+//   F2 rows: wave w owns the rows kr = 16 w + n; block c0 holds the inputs
+//      c1 = 4 q + e (c = c0 + 8 c1) -> spectrum S[16 w + n][4 q + t + 16 kc0].
+// The product with the filter spectrum (built by the same steps once per
+// workgroup, x 1/16384, fp32 registers) is lane-local.  The inverse is
+// conj(DFT2(conj(P))): conj(P) is written back in the image's layout (each
+// lane's four consecutive columns of its row as one 16-byte chunk) and the
+// same F1 / F2 run on it; conj of their result is staged the same way and
+// stored in 16-byte pieces.  Two LDS buffers swap roles per image (staging /
+// product / output in one, the exchange in the other): five workgroup
+// barriers per image.  2 x 66 KiB of buffers and the 14 KiB operand table
+// allow one workgroup per CU (2 waves per SIMD); the next image's pieces are
+// loaded while the current one is transformed.
+// Layouts (dwords = half2 values), conflict-free for every access in a bank
+// model checked on the CPU (16-byte accesses 16 lanes per cycle over 64
+// banks, dword reads 32 lanes per cycle over 32):
+//   image / product / output (r, c) at r 132 + c + 16 (r >> 5)
+//   exchange (kr, c) at c 132 + (kr ^ 16 ((c >> 5) & 1))
+// ---------------------------------------------------------------------------
+namespace conv2dm128 {
+constexpr int kStride = 132;
+constexpr int kBuf = 128 * kStride + 48;  // dwords per buffer
+__device__ __forceinline__ int rm_addr(int r, int c) { return r * kStride + c + 16 * (r >> 5); }
+__device__ __forceinline__ int cm_addr(int c, int kr) {
+    return c * kStride + (kr ^ (16 * ((c >> 5) & 1)));
+}
+
+// Operand table of the twiddled blocks j = 1..7, half h, lane (grouped
+// outputs k; output k, input i of block j is W128^(k (j + 8 i)), forward).
+constexpr int kOps = 7 * 2 * 64;  // u32x4 entries (14 KB)
+__device__ __forceinline__ int op_index(int j, int h, int lane) { return ((j - 1) * 2 + h) * 64 + lane; }
+
+// Entry e of the table, from the positive-angle table of length 128 (the
+// forward sign is its conjugate).  Row m of half h is output k = 4 (m / 4) +
+// 2 h + (m % 4) / 2, part (m % 4) % 2; column kk is input kk / 2, part kk % 2.
+__device__ __forceinline__ u32x4 op_entry(int e, const float2* __restrict__ tw128) {
+    const int lane = e & 63, h = (e >> 6) & 1, j = (e >> 7) + 1;
+    const int m = lane & 15, kq = lane >> 4;
+    const int o = m & 1;
+    const int k = 4 * (m >> 2) + 2 * h + ((m & 3) >> 1);
+    f16x8 r;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+        const int kk = 8 * kq + x;
+        const int in = kk >> 1, p = kk & 1;
+        const float2 w = tw128[(k * (j + 8 * in)) & 127];
+        const float c = w.x, sn = -w.y;
+        // out.re = c*in.re - s*in.im ; out.im = s*in.re + c*in.im
+        const float v = o == 0 ? (p == 0 ? c : -sn) : (p == 0 ? sn : c);
+        r[x] = static_cast<_Float16>(v);
+    }
+    return __builtin_bit_cast(u32x4, r);
+}
+
+// DFT8 over the block index of v[b][t] for every t (in-lane), forward.
+__device__ __forceinline__ void dft8_blocks(cpx (&v)[8][4]) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        cpx u[8];
+#pragma unroll
+        for (int b = 0; b < 8; ++b) u[b] = v[b][t];
+        Dft<8, true>::run(u);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k][t] = u[k];
+    }
+}
+
+// One 128-point stage over the 16 sequences of the lane's column n: block b
+// reads its inputs 4 q + e through addr(b, e).
+template <class Addr>
+__device__ __forceinline__ void stage128(const unsigned* src, Addr addr, const f16x8 (&ag)[2],
+                                         const u32x4* ops, int lane, cpx (&v)[8][4]) {
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        u32x4 xv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[e] = src[addr(b, e)];
+        f16x8 op[2];
+        if (b == 0) {
+            op[0] = ag[0];
+            op[1] = ag[1];
+        } else {
+            op[0] = __builtin_bit_cast(f16x8, ops[op_index(b, 0, lane)]);
+            op[1] = __builtin_bit_cast(f16x8, ops[op_index(b, 1, lane)]);
+        }
+        dft16_block(op, as_f16x8(xv), v[b]);
+    }
+    dft8_blocks(v);
+}
+
+// The 2-D forward transform of the values staged in `in` (rm_addr layout)
+// through the exchange buffer `fx` -> v[kc0][t] = S[16 w + n][4 q + t + 16 kc0].
+// `fx` is written with no barrier before: its previous readers must have
+// passed one.  Ends after the F2 reads (fx still being read by other waves).
+__device__ __forceinline__ void forward(const unsigned* in, unsigned* fx, const f16x8 (&ag)[2],
+                                        const u32x4* ops, int wave, int lane, cpx (&v)[8][4]) {
+    const int n = lane & 15, q = lane >> 4;
+    const int c = 16 * wave + n;
+    stage128(in, [&](int b, int e) { return rm_addr(b + 32 * q + 8 * e, c); }, ag, ops, lane, v);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        *reinterpret_cast<u32x4*>(fx + cm_addr(c, 4 * q + 16 * k)) =
+            u32x4{pack_half2(v[k][0]), pack_half2(v[k][1]), pack_half2(v[k][2]), pack_half2(v[k][3])};
+    __syncthreads();
+    stage128(fx, [&](int b, int e) { return cm_addr(b + 32 * q + 8 * e, c); }, ag, ops, lane, v);
+}
+
+// conj(v) of the lane's row 16 w + n into `buf` (rm_addr layout): columns
+// 4 q + t + 16 k, one 16-byte chunk per k.
+__device__ __forceinline__ void put_rows_conj(unsigned* buf, const cpx (&v)[8][4], int wave,
+                                              int lane) {
+    const int n = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+        *reinterpret_cast<u32x4*>(buf + rm_addr(16 * wave + n, 4 * q + 16 * k)) =
+            u32x4{pack_half2({v[k][0].re, -v[k][0].im}), pack_half2({v[k][1].re, -v[k][1].im}),
+                  pack_half2({v[k][2].re, -v[k][2].im}), pack_half2({v[k][3].re, -v[k][3].im})};
+}
+}  // namespace conv2dm128
+
+template <int kPerCu = 1>  // workgroups per CU (the LDS allows one)
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2 * kPerCu))) void
+conv2d128_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
+                      __half2* __restrict__ y, int batch, const float2* __restrict__ tw128,
+                      int tiles_per_block) {
+    using namespace conv2dm128;
+    constexpr int kImg = 128 * 128;
+    __shared__ __align__(16) unsigned buf[2][kBuf];
+    __shared__ u32x4 ops[kOps];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+
+    f16x8 ag[2];
+    dft16_operands_grouped<true>(ag, lane);
+    for (int e = tid; e < kOps; e += 512) ops[e] = op_entry(e, tw128);  // read after a barrier below
+
+    long long img, img_end, step;
+    tile_walk(batch, tiles_per_block, img, img_end, step);
+    if (img >= img_end) return;  // uniform over the workgroup
+
+    // An image's 16-byte pieces 4 tid + 2048 i (rows (4 tid + 2048 i) / 128).
+    auto load = [&](const __half2* src, u32x4 (&raw)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            raw[i] = ld_nt(reinterpret_cast<const u32x4*>(src + 4 * tid + 2048 * i));
+    };
+    auto stage = [&](unsigned* dst, const u32x4 (&raw)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int f = 4 * tid + 2048 * i;
+            *reinterpret_cast<u32x4*>(dst + rm_addr(f >> 7, f & 127)) = raw[i];
+        }
+    };
+
+    // The filter's spectrum / 16384 in the spectrum layout (buf[0] staging,
+    // buf[1] exchange; the first image then stages into buf[0], whose last
+    // readers passed the barrier inside forward).
+    cpx hs[8][4];
+    u32x4 next[8];
+    load(h, next);
+    stage(buf[0], next);
+    load(x + img * kImg, next);
+    __syncthreads();
+    forward(buf[0], buf[1], ag, ops, wave, lane, hs);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            hs[k][t] = {hs[k][t].re * (1.0f / kImg), hs[k][t].im * (1.0f / kImg)};
+
+    int s = 0;  // this image's staging buffer; the other is its exchange buffer
+    for (; img < img_end; img += step, s ^= 1) {
+        unsigned* const X = buf[s];
+        unsigned* const Y = buf[s ^ 1];
+        // X's last readers (the previous image's F1) passed a barrier since;
+        // Y's (its stores) pass the one after this staging.
+        stage(X, next);
+        if (img + step < img_end) load(x + (img + step) * kImg, next);
+        __syncthreads();
+        cpx v[8][4];
+        forward(X, Y, ag, ops, wave, lane, v);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[k][t] = cmul(v[k][t], hs[k][t]);
+        put_rows_conj(X, v, wave, lane);  // X's readers (F1) passed forward's barrier
+        __syncthreads();
+        forward(X, Y, ag, ops, wave, lane, v);  // Y's readers (F2) passed the last barrier
+        put_rows_conj(X, v, wave, lane);
+        __syncthreads();
+        __half2* dst = y + img * kImg;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int f = 4 * tid + 2048 * i;
+            st_nt(reinterpret_cast<u32x4*>(dst + f),
+                  *reinterpret_cast<const u32x4*>(X + rm_addr(f >> 7, f & 127)));
+        }
+    }
+}
+
+}  // namespace thff

@@ -424,17 +424,19 @@ hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y,
 #if THFF_N == 128
 hipError_t launch_conv2d128(int precision, const void* x, const void* h, void* y, int batch,
                             const float2* tw, int num_cus, hipStream_t stream) {
-    // One image per workgroup of 1024 lanes; the image's 140 KiB of LDS
-    // allow one per CU, so a device grid of one per CU walks the images.
+    // One image per workgroup: fp32 on VALU (1024 lanes, the image's 140 KiB
+    // of LDS), fp16 on MFMA (conv2d128_mfma_kernel: 512 lanes, 146 KiB of
+    // LDS); one workgroup per CU either way, so a device grid of one per CU
+    // walks the images grid-stride.
     const Grid g = make_grid(batch, 1, num_cus);
     if (precision == 0)
         conv2d128_kernel<float2><<<g.blocks, 1024, 0, stream>>>(
             static_cast<const float2*>(x), static_cast<const float2*>(h), static_cast<float2*>(y),
             batch, tw);
     else
-        conv2d128_kernel<__half2><<<g.blocks, 1024, 0, stream>>>(
+        conv2d128_mfma_kernel<1><<<g.blocks, 512, 0, stream>>>(
             static_cast<const __half2*>(x), static_cast<const __half2*>(h),
-            static_cast<__half2*>(y), batch, tw);
+            static_cast<__half2*>(y), batch, tw, g.tiles_per_block);
     return hipGetLastError();
 }
 #endif
