@@ -645,7 +645,19 @@ conv2d_cols_kernel(const In* in, Out* out, const float2* __restrict__ H, long lo
     constexpr long long blocks_per_image = C / Cols;
     constexpr int kAll = Block<In, R, Cols>::kCount;
 
-    auto where = [&](long long u, long long& base, int& c0) {
+    // A 128-byte line of a row holds kShare adjacent column blocks.  Work
+    // items u = b + k G are renamed within aligned groups of 8 kShare so that
+    // workgroups b, b + 8, b + 16, ... -- dispatched to the same XCD -- take
+    // the kShare blocks of one line: the line is then fetched into one XCD's
+    // L2 once instead of once per XCD (with consecutive blocks on consecutive
+    // XCDs, FETCH_SIZE read 2x the data for fp32, 4x for half).
+    constexpr int kShare = 128 / (Cols * static_cast<int>(sizeof(In))) > 1
+                               ? 128 / (Cols * static_cast<int>(sizeof(In))) : 1;
+    constexpr int kGroup = 8 * kShare;
+    static_assert(blocks_per_image % kGroup == 0, "column blocks per image: whole groups");
+    auto where = [&](long long u0, long long& base, int& c0) {
+        const int i = static_cast<int>(u0 % kGroup);
+        const long long u = u0 - i + kShare * (i % 8) + i / 8;
         const long long img = u / blocks_per_image;
         c0 = static_cast<int>(u - img * blocks_per_image) * Cols;
         base = img * R * static_cast<long long>(cols) + c0;
