@@ -380,163 +380,205 @@ conv2d64_kernel(const IO* __restrict__ x, const IO* __restrict__ h, IO* __restri
 }
 
 // ---------------------------------------------------------------------------
-// 2-D circular convolution of 128 x 128 images with one shared filter (the
-// contract of conv2d64_kernel; the reference's 128-tile sketch is
-// sample/conv2d/thunder_tile128.cu:64-237): one image per workgroup of 1024
-// lanes (16 waves), the image held in LDS in fp32, row-major, element (r, c)
-// at r * kStride + lds_pad(c) (140 KiB, so one workgroup per CU):
-//   rows:    wave w owns rows 8 w .. 8 w + 7; lane (r, t) = (8 w + l / 8, l % 8)
-//            holds x[r][t + 8 j], j < 16, and runs the length-128 transform
-//            with the row itself as its slot (wave-scope syncs only);
-//   barrier;
-//   columns: lane (c, t) = (tid / 8, tid % 8) transforms column c where it
-//            lies (StridedSlot, stride kStride; the 8 lanes of a column are
-//            one wave's, so again wave-scope syncs only): forward, times the
-//            filter spectrum / 16384 (fp32 registers, same layout), inverse;
-//   barrier;
-//   rows:    the inverse row transforms, out.
-// Each wave moves its own 8 rows (8 KiB fp32, 4 KiB half) between HBM and LDS
-// in 16-byte pieces, so staging needs no workgroup barrier: two barriers per
-// image.  The next image's pieces are loaded before the current image is
-// transformed.  kStride = 140 (2 * 140 = 24 mod 64 banks) keeps the column
-// reads of a half-wave (8 rows t + 8 j by 4 columns) on distinct banks.
-// The filter spectrum is computed per workgroup at set-up, as the first half
-// of an image.
+// fp32 2-D circular convolution of 128 x 128 images with one shared filter
+// (y = IFFT2(FFT2(x) * FFT2(h)) / 16384, the contract of conv2d64_kernel; the
+// reference's 128-tile sketch is sample/conv2d/thunder_tile128.cu:64-237) in
+// four lane layouts, one image per 1024-lane workgroup, 16 values per lane.
+// Both indices split as r = r0 + 8 r1, c = c0 + 8 c1 (r0, c0 < 8), and each
+// wave has one digit u = w mod 8 that is constant over its lanes, so every
+// twiddle it applies is one of 16 wave-uniform values W128^(u k):
+//   L0  lane (r0 = u, c = 64 (w / 8) + l): x[r0 + 8 j][c], j = r1 -- loaded
+//       and stored straight from registers, each instruction 64 consecutive
+//       values of one row; DFT16 over r1, times W128^(r0 kr1);
+//   L1  lane (kr1 in {u, u + 8}, c): the 8 values over r0 of both kr1 (an
+//       exchange within the 8 waves of one column half); two DFT8 over r0
+//       -> X[kr = kr1 + 16 kr0][c];
+//   L2  lane (c0 = u, kr = 64 (w / 8) + l): X[kr][c0 + 8 j], j = c1 (the
+//       transpose, through a column-major buffer of stride 129); DFT16 over
+//       c1, times W128^(c0 kc1);
+//   L3  lane (kc1 in {u, u + 8}, kr): the 8 values over c0 of both kc1; two
+//       DFT8 over c0 -> spectrum S[kr][kc1 + 16 kc0].
+// The product with the filter spectrum (the same steps on h once per
+// workgroup, x 1/16384, fp32 registers) is lane-local, and the inverse runs
+// the steps backwards.  Every exchange moves 8-byte values with 64
+// consecutive lanes on 64 consecutive (or 129-strided) slots: no bank
+// conflicts.  One 129 KiB buffer serves all six exchanges, each between two
+// workgroup barriers; the next image is loaded into registers while the
+// current one is transformed (half before the forward transform, half
+// before the inverse: 127 VGPRs, no spill).  2048 images on MI355X: 134 us,
+// against 183 us for a row/column form that kept the image in LDS (two
+// barriers per image, but only a quarter of the next image prefetched).
 // ---------------------------------------------------------------------------
-namespace conv2d128 {
-inline constexpr int kN = 128;
-inline constexpr int kStride = 140;
-inline constexpr int kLds = kN * kStride;  // cpx
-inline constexpr int kLanes = 1024;
+namespace conv2d128l {
+constexpr int kN = 128;
+constexpr int kT = 129;  // column stride of the transpose buffer
+constexpr int kLds = kN * kT;
 
-template <class IO>
-struct Pieces {
-    static constexpr int kVec = Io<IO>::kVec;
-    static constexpr int kCount = 1024 / (64 * kVec);  // 16-byte pieces per lane (8 / 4)
-    typename Io<IO>::W4 w[kCount];
-};
-
-// Pieces [First, Last) of the wave's 8 rows of image img: piece i holds
-// values 1024 w + kVec l + 64 kVec i.
-template <int First, int Last, class IO>
-__device__ __forceinline__ void load(Pieces<IO>& p, const IO* __restrict__ base, long long img,
-                                     int wave, int lane) {
-    using W = typename Io<IO>::W4;
-    const IO* src = base + img * (kN * kN) + 1024 * wave + Pieces<IO>::kVec * lane;
-#pragma unroll
-    for (int i = First; i < Last; ++i)
-        p.w[i] = ld_nt(reinterpret_cast<const W*>(src + 64 * Pieces<IO>::kVec * i));
-}
-
-// Pieces of the next image loaded before the current one is transformed (the
-// rest right after its store): with the image (32 VGPRs) and its filter
-// spectrum (32) live, two pieces fit the 128 VGPRs of 4 waves per SIMD
-// without spilling in both types (three spill 8 bytes).
-template <class IO>
-inline constexpr int kEarly = 2;
-
-template <class IO>
-__device__ __forceinline__ void stage(const Pieces<IO>& p, cpx* lds, int wave, int lane) {
-    constexpr int kVec = Pieces<IO>::kVec;
-#pragma unroll
-    for (int i = 0; i < Pieces<IO>::kCount; ++i) {
-        const int e = 1024 * wave + kVec * lane + 64 * kVec * i;  // image value
-        cpx q[kVec];
-        Io<IO>::decode4(p.w[i], q);
-#pragma unroll
-        for (int c = 0; c < kVec; ++c) lds[(e >> 7) * kStride + lds_pad((e & 127) + c)] = q[c];
-    }
-}
-
-template <class IO>
-__device__ __forceinline__ void store(IO* __restrict__ base, long long img, const cpx* lds,
-                                      int wave, int lane) {
-    using W = typename Io<IO>::W4;
-    constexpr int kVec = Pieces<IO>::kVec;
-    IO* dst = base + img * (kN * kN) + 1024 * wave + kVec * lane;
-#pragma unroll
-    for (int i = 0; i < Pieces<IO>::kCount; ++i) {
-        const int e = 1024 * wave + kVec * lane + 64 * kVec * i;
-        cpx q[kVec];
-#pragma unroll
-        for (int c = 0; c < kVec; ++c) q[c] = lds[(e >> 7) * kStride + lds_pad((e & 127) + c)];
-        st_nt(reinterpret_cast<W*>(dst + 64 * kVec * i), Io<IO>::encode4(q));
-    }
-}
-
-// Row r of the image as the length-128 transform slot of its 8 lanes.
+// a[k] *= t[k] (forward) or conj(t[k]) for k = 1..15 (the wave-uniform
+// factors of this layout).
 template <bool FWD>
-__device__ __forceinline__ void rows(cpx* lds, int r, int t, const LaneTwiddles<kN>& w) {
-    cpx* row = lds + r * kStride;
-    cpx v[16];
-    wave_lds_sync();
+__device__ __forceinline__ void twiddle(cpx (&a)[16], const cpx (&t)[16]) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = row[lds_pad(t + 8 * j)];
-    fft_registers<kN, FWD>(v, row, t, w);
-    wave_lds_sync();
-#pragma unroll
-    for (int j = 0; j < 16; ++j) row[lds_pad(t + 8 * j)] = v[j];
+    for (int k = 1; k < 16; ++k) a[k] = FWD ? cmul(a[k], t[k]) : cmulc(a[k], t[k]);
 }
-}  // namespace conv2d128
 
-template <class IO>
-__global__ __launch_bounds__(1024) void conv2d128_kernel(const IO* __restrict__ x,
-                                                         const IO* __restrict__ h,
-                                                         IO* __restrict__ y, int batch,
-                                                         const float2* __restrict__ tw) {
-    using namespace conv2d128;
-    __shared__ cpx lds[kLds];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int t = tid & 7;
-    const int r = 8 * wave + (lane >> 3);  // row of the row phases
-    const int c = tid >> 3;                // column of the column phase
-    const StridedSlot col{lds + lds_pad(c), kStride};
-    LaneTwiddles<kN> w;
-    w.load(t, tw);
-    constexpr int kE = kEarly<IO>, kAll = Pieces<IO>::kCount;
+// The forward 2-D DFT of the image held in L0 order (a[j] = x[u + 8 j][c]),
+// through L: on return a[8 s + kc0] = S[kr][u + 8 s + 16 kc0], kr = c.
+__device__ __forceinline__ void forward(cpx (&a)[16], cpx* L, int u, int c, const cpx (&t)[16]) {
+    Dft<16, true>::run(a);
+    twiddle<true>(a, t);
+    __syncthreads();  // earlier readers of L are done
+#pragma unroll
+    for (int k = 0; k < 16; ++k) L[(u * 16 + k) * kN + c] = a[k];
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) a[8 * s + r] = L[(r * 16 + u + 8 * s) * kN + c];
+    Dft<8, true>::run(a);
+    Dft<8, true>::run(a + 8);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) L[c * kT + u + 8 * s + 16 * k] = a[8 * s + k];
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 16; ++j) a[j] = L[(u + 8 * j) * kT + c];
+    Dft<16, true>::run(a);
+    twiddle<true>(a, t);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) L[(u * 16 + k) * kN + c] = a[k];
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) a[8 * s + r] = L[(r * 16 + u + 8 * s) * kN + c];
+    Dft<8, true>::run(a);
+    Dft<8, true>::run(a + 8);
+}
 
+// The inverse of forward (unnormalized): spectrum order in, L0 order out.
+__device__ __forceinline__ void inverse(cpx (&a)[16], cpx* L, int u, int c, const cpx (&t)[16]) {
+    Dft<8, false>::run(a);
+    Dft<8, false>::run(a + 8);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) L[(r * 16 + u + 8 * s) * kN + c] = a[8 * s + r];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) a[k] = L[(u * 16 + k) * kN + c];
+    twiddle<false>(a, t);
+    Dft<16, false>::run(a);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 16; ++j) L[(u + 8 * j) * kT + c] = a[j];
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) a[8 * s + k] = L[c * kT + u + 8 * s + 16 * k];
+    Dft<8, false>::run(a);
+    Dft<8, false>::run(a + 8);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) L[(r * 16 + u + 8 * s) * kN + c] = a[8 * s + r];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) a[k] = L[(u * 16 + k) * kN + c];
+    twiddle<false>(a, t);
+    Dft<16, false>::run(a);
+}
+}  // namespace conv2d128l
+
+template <int kUnused = 0>
+__global__ __launch_bounds__(1024) void conv2d128_lanes_kernel(const float2* __restrict__ x,
+                                                               const float2* __restrict__ h,
+                                                               float2* __restrict__ y, int batch,
+                                                               const float2* __restrict__ tw) {
+    using namespace conv2d128l;
+    constexpr int kImg = kN * kN;
+    __shared__ cpx L[kLds];
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int u = w & 7;
+    const int c = 64 * (w >> 3) + (tid & 63);
+    // W128^(u k) (forward: the conjugate of the positive-angle table).
+    cpx t[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const float2 v = tw[(u * k) & (kN - 1)];
+        t[k] = {v.x, -v.y};
+    }
     long long img, img_end, step;
     tile_walk(batch, 0, img, img_end, step);
     if (img >= img_end) return;  // uniform over the workgroup
 
-    // The filter's spectrum / 16384 in the column layout: hs[j] = H[t + 8 j][c].
-    Pieces<IO> raw;
-    load<0, kAll>(raw, h, 0, wave, lane);
-    stage(raw, lds, wave, lane);
-    load<0, kAll>(raw, x, img, wave, lane);
-    rows<true>(lds, r, t, w);
-    __syncthreads();
-    cpx hs[16];
+    auto load = [&](const float2* src, cpx (&a)[16]) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) hs[j] = slot_at(col, t + 8 * j);
-    fft_registers<kN, true>(hs, col, t, w);
-    constexpr float kScale = 1.0f / (kN * kN);
+        for (int j = 0; j < 16; ++j) {
+            const u32x2 v = ld_nt(reinterpret_cast<const u32x2*>(src + (u + 8 * j) * kN + c));
+            a[j] = Io<float2>::decode1(v);
+        }
+    };
+    // The image's values and the next image's alternate between two register
+    // sets (the loop is unrolled by two, so no set is copied): the next
+    // image's loads are issued before the current one is transformed, with
+    // no branch (the last pass reloads its own image), and 16 stores to a
+    // resource of no bytes after the first loads make the loop's entry look
+    // like every later pass (the loads followed by 16 stores in flight), so
+    // the compiler waits at the top of a pass for that pass's loads only,
+    // not for the previous image's stores.
+    // Buffer accesses: the image's resource in scalar registers, the lane's
+    // offset in one VGPR, the row step j in the scalar offset.
+    const int voff = 8 * (u * kN + c);
+    auto load_img = [&](long long im, cpx (&a)[16], int j0 = 0, int j1 = 16) {
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float2*>(x + im * kImg), 0, kImg * 8, 0x00020000);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) hs[j] = {hs[j].re * kScale, hs[j].im * kScale};
-    __syncthreads();  // every column read of the filter is done
-
-    for (; img < img_end; img += step) {
-        const bool next = img + step < img_end;
-        wave_lds_sync();
-        stage(raw, lds, wave, lane);
-        if (next) load<0, kE>(raw, x, img + step, wave, lane);
-        rows<true>(lds, r, t, w);
-        __syncthreads();
-        cpx v[16];
+        for (int j = j0; j < j1; ++j)
+            a[j] = Io<float2>::decode1(__builtin_bit_cast(
+                u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, voff, 64 * kN * j, 2)));
+    };
+    cpx hs[16], va[16], vb[16];
+    load(h, hs);
+    load_img(img, va);
+    {
+        const __amdgpu_buffer_rsrc_t none =
+            __builtin_amdgcn_make_buffer_rsrc(y, 0, batch < 0 ? 16 : 0, 0x00020000);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = slot_at(col, t + 8 * j);
-        fft_registers<kN, true>(v, col, t, w);
+        for (int j = 0; j < 16; ++j)
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{}, none, 0, 64 * kN * j, 2);
+    }
+    forward(hs, L, u, c, t);
+    constexpr float kScale = 1.0f / kImg;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = cmul(v[j], hs[j]);
-        fft_registers<kN, false>(v, col, t, w);
-        wave_lds_sync();
+    for (int k = 0; k < 16; ++k) hs[k] = {hs[k].re * kScale, hs[k].im * kScale};
+    auto pass = [&](cpx (&a)[16], cpx (&nxt)[16]) {
+        const long long nim = img + step < img_end ? img + step : img;
+        load_img(nim, nxt, 0, 8);
+        forward(a, L, u, c, t);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) slot_at(col, t + 8 * j) = v[j];
-        __syncthreads();
-        rows<false>(lds, r, t, w);
-        wave_lds_sync();
-        store(y, img, lds, wave, lane);
-        if (next) load<kE, kAll>(raw, x, img + step, wave, lane);
+        for (int k = 0; k < 16; ++k) a[k] = cmul(a[k], hs[k]);
+        load_img(nim, nxt, 8, 16);
+        inverse(a, L, u, c, t);
+        const __amdgpu_buffer_rsrc_t ys =
+            __builtin_amdgcn_make_buffer_rsrc(y + img * kImg, 0, kImg * 8, 0x00020000);
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            __builtin_amdgcn_raw_buffer_store_b64(Io<float2>::encode1(a[j]), ys, voff, 64 * kN * j, 2);
+        img += step;
+    };
+    while (img < img_end) {
+        pass(va, vb);
+        if (img >= img_end) break;
+        pass(vb, va);
     }
 }
 

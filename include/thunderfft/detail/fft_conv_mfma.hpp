@@ -1412,7 +1412,7 @@ namespace thff {
 
 // ---------------------------------------------------------------------------
 // half2 2-D convolution of 128 x 128 images on MFMA (the contract of
-// conv2d128_kernel: y = IFFT2(FFT2(x) * FFT2(h)) / 16384, one shared filter;
+// conv2d128_lanes_kernel: y = IFFT2(FFT2(x) * FFT2(h)) / 16384, one shared filter;
 // the reference's 128-tile sketch is sample/conv2d/thunder_tile128.cu:64-237),
 // one image per workgroup tile of 512 lanes (8 waves).  Both 128-point
 // transforms split as 128 = 16 x 8: a DFT16 on v_mfma_f32_16x16x32_f16 over

@@ -424,13 +424,13 @@ hipError_t launch_conv2d64(int precision, const void* x, const void* h, void* y,
 #if THFF_N == 128
 hipError_t launch_conv2d128(int precision, const void* x, const void* h, void* y, int batch,
                             const float2* tw, int num_cus, hipStream_t stream) {
-    // One image per workgroup: fp32 on VALU (1024 lanes, the image's 140 KiB
-    // of LDS), fp16 on MFMA (conv2d128_mfma_kernel: 512 lanes, 146 KiB of
-    // LDS); one workgroup per CU either way, so a device grid of one per CU
-    // walks the images grid-stride.
+    // One image per workgroup: fp32 on VALU (conv2d128_lanes_kernel: 1024
+    // lanes, a 129 KiB exchange buffer), fp16 on MFMA (conv2d128_mfma_kernel:
+    // 512 lanes, 146 KiB of LDS); one workgroup per CU either way, so a device
+    // grid of one per CU walks the images grid-stride.
     const Grid g = make_grid(batch, 1, num_cus);
     if (precision == 0)
-        conv2d128_kernel<float2><<<g.blocks, 1024, 0, stream>>>(
+        conv2d128_lanes_kernel<><<<g.blocks, 1024, 0, stream>>>(
             static_cast<const float2*>(x), static_cast<const float2*>(h), static_cast<float2*>(y),
             batch, tw);
     else
