@@ -610,20 +610,20 @@ namespace conv2dcols {
 template <int R>
 inline constexpr int kSlotStride = C2CPlan<R>::kSlot + 4;
 
-// Cols columns per unit (one per wave: 64 Cols lanes).
-template <class IO, int R, int Cols>
+// Cols columns per unit, moved by kLanes lanes in 16-byte row pieces.
+template <class IO, int R, int Cols, int kLanes = 64 * Cols>
 struct Block {
     static constexpr int kVec = Io<IO>::kVec;
     static constexpr int kPer = Cols / kVec;                 // pieces per row
-    static constexpr int kRowsPerStep = 64 * Cols / kPer;    // rows per lane step
+    static constexpr int kRowsPerStep = kLanes / kPer;       // rows per lane step
     static constexpr int kCount = R / kRowsPerStep;     // pieces per lane
     typename Io<IO>::W4 w[kCount];
 };
 
-template <int First, int Last, int C, class IO, int R, int Cols>
-__device__ __forceinline__ void load(Block<IO, R, Cols>& b, const IO* in, long long base, int tid) {
+template <int First, int Last, int C, class IO, int R, int Cols, int L>
+__device__ __forceinline__ void load(Block<IO, R, Cols, L>& b, const IO* in, long long base, int tid) {
     constexpr long long cols = C;
-    using B = Block<IO, R, Cols>;
+    using B = Block<IO, R, Cols, L>;
     const int p = tid % B::kPer, r0 = tid / B::kPer;
 #pragma unroll
     for (int i = First; i < Last; ++i) {
@@ -632,9 +632,9 @@ __device__ __forceinline__ void load(Block<IO, R, Cols>& b, const IO* in, long l
     }
 }
 
-template <class IO, int R, int Cols>
-__device__ __forceinline__ void stage(const Block<IO, R, Cols>& b, cpx* lds, int tid) {
-    using B = Block<IO, R, Cols>;
+template <class IO, int R, int Cols, int L>
+__device__ __forceinline__ void stage(const Block<IO, R, Cols, L>& b, cpx* lds, int tid) {
+    using B = Block<IO, R, Cols, L>;
     const int p = tid % B::kPer, r0 = tid / B::kPer;
 #pragma unroll
     for (int i = 0; i < B::kCount; ++i) {
@@ -646,10 +646,10 @@ __device__ __forceinline__ void stage(const Block<IO, R, Cols>& b, cpx* lds, int
     }
 }
 
-template <int C, class IO, int R, int Cols>
+template <int C, class IO, int R, int Cols, int L = 64 * Cols>
 __device__ __forceinline__ void store(IO* out, long long base, const cpx* lds, int tid) {
     constexpr long long cols = C;
-    using B = Block<IO, R, Cols>;
+    using B = Block<IO, R, Cols, L>;
     const int p = tid % B::kPer, r0 = tid / B::kPer;
 #pragma unroll
     for (int i = 0; i < B::kCount; ++i) {
@@ -663,29 +663,36 @@ __device__ __forceinline__ void store(IO* out, long long base, const cpx* lds, i
 }
 }  // namespace conv2dcols
 
-// Waves per SIMD: 8 columns per unit (512 lanes) hold two, with the next
-// unit's block prefetched; 4 columns (256 lanes) three, loading each block
-// when its unit starts (the prefetch would spill there).
+// Waves per SIMD: 8 columns per unit (512 lanes, one wave per column) hold
+// two, with the next unit's block prefetched; 16 columns (512 lanes, two
+// columns per wave) two, loading each block when its unit starts (the
+// prefetch would spill there); 4 columns (256 lanes) three, likewise.
 template <int Cols>
-inline constexpr int kColsWavesPerEU = Cols == 8 ? 2 : 3;
+inline constexpr int kColsWavesPerEU = Cols == 8 || Cols == 16 ? 2 : 3;
 template <int Cols>
 inline constexpr bool kColsPrefetch = Cols == 8;
+// Lanes per workgroup: one wave per column up to 8 columns; 16 columns are
+// 8 waves of two columns each.
+template <int Cols>
+inline constexpr int kColsLanes = Cols <= 8 ? 64 * Cols : 512;
 
 template <class In, class Out, int R, int C, bool kConv, int Cols>
-__global__ __launch_bounds__(64 * Cols) __attribute__((amdgpu_waves_per_eu(kColsWavesPerEU<Cols>))) void
+__global__ __launch_bounds__(kColsLanes<Cols>) __attribute__((amdgpu_waves_per_eu(kColsWavesPerEU<Cols>))) void
 conv2d_cols_kernel(const In* in, Out* out, const float2* __restrict__ H, long long units,
                    float scale, const float2* __restrict__ tw) {
     using P = C2CPlan<R>;
     static_assert(P::kTPF == 64, "one wave per column");
     using namespace conv2dcols;
+    constexpr int kL = kColsLanes<Cols>;
+    constexpr int kWaves = kL / 64;
+    constexpr int kCPW = Cols / kWaves;  // columns per wave
     __shared__ __align__(16) cpx lds[Cols * kSlotStride<R>];
     const int tid = threadIdx.x, wave = tid >> 6, t = tid & 63;
     LaneTwiddles<R> w;
     w.load(t, tw);
-    cpx* const slot = lds + wave * kSlotStride<R>;
     constexpr long long cols = C;
     constexpr long long blocks_per_image = C / Cols;
-    constexpr int kAll = Block<In, R, Cols>::kCount;
+    constexpr int kAll = Block<In, R, Cols, kL>::kCount;
 
     // A 128-byte line of a row holds kShare adjacent column blocks.  Work
     // items u = b + k G are renamed within aligned groups of 8 kShare so that
@@ -709,10 +716,10 @@ conv2d_cols_kernel(const In* in, Out* out, const float2* __restrict__ H, long lo
     long long base;
     int c0;
     where(u, base, c0);
-    Block<In, R, Cols> raw;
+    Block<In, R, Cols, kL> raw;
     if constexpr (kColsPrefetch<Cols>) load<0, kAll, C>(raw, in, base, tid);
     int h_c0 = -1;
-    cpx hs[kConv ? 16 : 1];
+    cpx hs[kCPW][kConv ? 16 : 1];
     for (; u < units; u += gridDim.x) {
         const long long next_u = u + gridDim.x;
         long long next_base = 0;
@@ -725,33 +732,40 @@ conv2d_cols_kernel(const In* in, Out* out, const float2* __restrict__ H, long lo
             if (next_u < units) load<0, kAll, C>(raw, in, next_base, tid);
         if constexpr (kConv) {
             if (c0 != h_c0) {  // uniform: this workgroup's column block changed
-                const float2* hc = H + c0 + wave;
 #pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const float2 hk = hc[static_cast<long long>(t + 64 * j) * cols];
-                    hs[j] = {hk.x, hk.y};
+                for (int v = 0; v < kCPW; ++v) {
+                    const float2* hc = H + c0 + wave + kWaves * v;
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        const float2 hk = hc[static_cast<long long>(t + 64 * j) * cols];
+                        hs[v][j] = {hk.x, hk.y};
+                    }
                 }
                 h_c0 = c0;
             }
         }
         __syncthreads();
-        cpx v[16];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = slot[lds_pad(t + 64 * j)];
-        fft_registers<R, true>(v, slot, t, w);
-        if constexpr (kConv) {
+        for (int cv = 0; cv < kCPW; ++cv) {
+            cpx* const slot = lds + (wave + kWaves * cv) * kSlotStride<R>;
+            cpx v[16];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) v[j] = cmul(v[j], hs[j]);
-            fft_registers<R, false>(v, slot, t, w);
-        } else {
+            for (int j = 0; j < 16; ++j) v[j] = slot[lds_pad(t + 64 * j)];
+            fft_registers<R, true>(v, slot, t, w);
+            if constexpr (kConv) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) v[j] = {v[j].re * scale, v[j].im * scale};
+                for (int j = 0; j < 16; ++j) v[j] = cmul(v[j], hs[cv][j]);
+                fft_registers<R, false>(v, slot, t, w);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) v[j] = {v[j].re * scale, v[j].im * scale};
+            }
+            wave_lds_sync();
+#pragma unroll
+            for (int j = 0; j < 16; ++j) slot[lds_pad(t + 64 * j)] = v[j];
         }
-        wave_lds_sync();
-#pragma unroll
-        for (int j = 0; j < 16; ++j) slot[lds_pad(t + 64 * j)] = v[j];
         __syncthreads();
-        store<C, Out, R, Cols>(out, base, lds, tid);
+        store<C, Out, R, Cols, kL>(out, base, lds, tid);
         base = next_base;
         c0 = next_c0;
     }

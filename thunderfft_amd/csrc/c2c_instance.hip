@@ -446,36 +446,46 @@ hipError_t launch_conv2d_cols(int precision, bool conv, const void* in, void* ou
                               const float2* H, int cols, long long images, float scale,
                               const float2* tw, int num_cus, hipStream_t stream) {
     if (cols != 1024) return hipErrorInvalidValue;  // the kernels are built for 1024 columns
-    // kCols columns per unit, one wave per column; workgroups walk the units
-    // grid-stride, and the grid is a multiple of the image's column blocks, so
-    // every workgroup keeps one column block (and its H column).  Measured on
-    // MI355X, 32 images of 1024 x 1024 end to end: 8 columns (64-byte row
-    // pieces fp32, one 512-lane workgroup per CU with the next block
-    // prefetched) 419 us fp32 / 394 us half, against 790 / 662 us with 4
-    // columns (32-byte pieces, three 256-lane workgroups per CU).
-    constexpr int kCols = 8;
-    constexpr int kPerCu = kColsWavesPerEU<kCols> * 4 / kCols;
-    const long long blocks_per_image = cols / kCols;
-    const long long units = blocks_per_image * images;
-    long long grid = static_cast<long long>(kPerCu) * (num_cus > 0 ? num_cus : 256);
-    if (grid >= blocks_per_image) grid -= grid % blocks_per_image;
-    const dim3 blocks(static_cast<unsigned>(units < grid ? units : grid));
-    const dim3 lanes(64 * kCols);
-    if (precision == 0) {
-        if (conv)
-            conv2d_cols_kernel<float2, float2, 1024, 1024, true, kCols><<<blocks, lanes, 0, stream>>>(
-                static_cast<const float2*>(in), static_cast<float2*>(out), H, units, scale, tw);
-        else
-            conv2d_cols_kernel<float2, float2, 1024, 1024, false, kCols><<<blocks, lanes, 0, stream>>>(
-                static_cast<const float2*>(in), static_cast<float2*>(out), H, units, scale, tw);
-    } else {
-        if (conv)
-            conv2d_cols_kernel<__half2, __half2, 1024, 1024, true, kCols><<<blocks, lanes, 0, stream>>>(
-                static_cast<const __half2*>(in), static_cast<__half2*>(out), H, units, scale, tw);
-        else
-            conv2d_cols_kernel<__half2, float2, 1024, 1024, false, kCols><<<blocks, lanes, 0, stream>>>(
-                static_cast<const __half2*>(in), static_cast<float2*>(out), H, units, scale, tw);
-    }
+    // kCols columns per unit (one wave per column for fp32, two per wave for
+    // half); workgroups walk the units grid-stride, and the grid is a multiple
+    // of the image's column blocks, so every workgroup keeps one column block
+    // (and its H columns).  The unit's rows move as 16-byte pieces, 64 bytes
+    // of each row (fp32: 8 columns; half: 16), through one 512-lane workgroup
+    // per CU.  Measured on MI355X, 32 images of 1024 x 1024 end to end: fp32
+    // 8 columns with the next block prefetched 359 us (16 columns, two per
+    // wave, no prefetch: 358 us, 124 bytes of spill); half 16 columns 253 us
+    // against 277 us with 8 columns (32-byte pieces: a wave's loads then touch
+    // twice the rows); one column per wave on MFMA with 16-byte pieces (4
+    // columns per 256-lane workgroup) 545 us.
+    auto launch = [&](auto cols_tag, const void* src, void* dst) {
+        constexpr int kCols = decltype(cols_tag)::value;
+        constexpr int kPerCu = kColsWavesPerEU<kCols> * 4 / (kColsLanes<kCols> / 64);
+        const long long blocks_per_image = cols / kCols;
+        const long long units = blocks_per_image * images;
+        long long grid = static_cast<long long>(kPerCu) * (num_cus > 0 ? num_cus : 256);
+        if (grid >= blocks_per_image) grid -= grid % blocks_per_image;
+        const dim3 blocks(static_cast<unsigned>(units < grid ? units : grid));
+        const dim3 lanes(kColsLanes<kCols>);
+        if (precision == 0) {
+            if (conv)
+                conv2d_cols_kernel<float2, float2, 1024, 1024, true, kCols><<<blocks, lanes, 0, stream>>>(
+                    static_cast<const float2*>(src), static_cast<float2*>(dst), H, units, scale, tw);
+            else
+                conv2d_cols_kernel<float2, float2, 1024, 1024, false, kCols><<<blocks, lanes, 0, stream>>>(
+                    static_cast<const float2*>(src), static_cast<float2*>(dst), H, units, scale, tw);
+        } else {
+            if (conv)
+                conv2d_cols_kernel<__half2, __half2, 1024, 1024, true, kCols><<<blocks, lanes, 0, stream>>>(
+                    static_cast<const __half2*>(src), static_cast<__half2*>(dst), H, units, scale, tw);
+            else
+                conv2d_cols_kernel<__half2, float2, 1024, 1024, false, kCols><<<blocks, lanes, 0, stream>>>(
+                    static_cast<const __half2*>(src), static_cast<float2*>(dst), H, units, scale, tw);
+        }
+    };
+    if (precision == 0)
+        launch(std::integral_constant<int, 8>{}, in, out);
+    else
+        launch(std::integral_constant<int, 16>{}, in, out);
     return hipGetLastError();
 }
 #endif
