@@ -529,7 +529,8 @@ __global__ __launch_bounds__(1024) void conv2d128_lanes_kernel(const float2* __r
     // The image's values and the next image's alternate between two register
     // sets (the loop is unrolled by two, so no set is copied): the next
     // image's loads are issued before the current one is transformed, with
-    // no branch (the last pass reloads its own image), and 16 stores to a
+    // no branch (the last pass's go through a resource of no bytes and read
+    // zeros without touching memory), and 16 stores to a
     // resource of no bytes after the first loads make the loop's entry look
     // like every later pass (the loads followed by 16 stores in flight), so
     // the compiler waits at the top of a pass for that pass's loads only,
@@ -537,9 +538,9 @@ __global__ __launch_bounds__(1024) void conv2d128_lanes_kernel(const float2* __r
     // Buffer accesses: the image's resource in scalar registers, the lane's
     // offset in one VGPR, the row step j in the scalar offset.
     const int voff = 8 * (u * kN + c);
-    auto load_img = [&](long long im, cpx (&a)[16], int j0 = 0, int j1 = 16) {
+    auto load_img = [&](long long im, cpx (&a)[16], int j0 = 0, int j1 = 16, bool live = true) {
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float2*>(x + im * kImg), 0, kImg * 8, 0x00020000);
+            const_cast<float2*>(x + im * kImg), 0, live ? kImg * 8 : 0, 0x00020000);
 #pragma unroll
         for (int j = j0; j < j1; ++j)
             a[j] = Io<float2>::decode1(__builtin_bit_cast(
@@ -561,12 +562,13 @@ __global__ __launch_bounds__(1024) void conv2d128_lanes_kernel(const float2* __r
 #pragma unroll
     for (int k = 0; k < 16; ++k) hs[k] = {hs[k].re * kScale, hs[k].im * kScale};
     auto pass = [&](cpx (&a)[16], cpx (&nxt)[16]) {
-        const long long nim = img + step < img_end ? img + step : img;
-        load_img(nim, nxt, 0, 8);
+        const bool live = img + step < img_end;
+        const long long nim = live ? img + step : img;
+        load_img(nim, nxt, 0, 8, live);
         forward(a, L, u, c, t);
 #pragma unroll
         for (int k = 0; k < 16; ++k) a[k] = cmul(a[k], hs[k]);
-        load_img(nim, nxt, 8, 16);
+        load_img(nim, nxt, 8, 16, live);
         inverse(a, L, u, c, t);
         const __amdgpu_buffer_rsrc_t ys =
             __builtin_amdgcn_make_buffer_rsrc(y + img * kImg, 0, kImg * 8, 0x00020000);
