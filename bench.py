@@ -548,6 +548,32 @@ def _profile_value(path: str, field: str, key: str):
     return m.group(1) if m else None
 
 
+def kernel_sources_sha16() -> str:
+    """First 16 hex digits of the sha256 of the kernel sources (every
+    include/thunderfft/detail/*.hpp and thunderfft_amd/csrc/* file, sorted by
+    path): the profile summaries record the value they were measured with."""
+    import glob
+    import hashlib
+
+    files = sorted(glob.glob(os.path.join(ROOT, "include", "thunderfft", "detail", "*.hpp")) +
+                   glob.glob(os.path.join(ROOT, "thunderfft_amd", "csrc", "*")))
+    h = hashlib.sha256()
+    for f in files:
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def profile_sources(path: str):
+    """The kernel_sources_sha16 a profile summary was measured with, or None."""
+    try:
+        with open(path) as f:
+            m = re.search(r"^kernel_sources_sha16: ([0-9a-f]+)\s*$", f.read(), re.M)
+    except OSError:
+        return None
+    return m.group(1) if m else None
+
+
 def load_traffic(key: str):
     """HBM bytes per launch for `key` (e.g. float_fwd) from the PMC summary."""
     v = _profile_value(TRAFFIC_PROFILE, "hbm_bytes_per_launch", key)
@@ -742,11 +768,23 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": load_traffic("float_fwd"),
                      "kernel": "thff::c2c_kernel<float2, 1024, true, false, false>",
-                     "algorithmic_bytes": main_run["bytes_per_call"]},
+                     "algorithmic_bytes": main_run["bytes_per_call"],
+                     "traffic_profile": "profiles/pmc_c2c_n1024_b65536.md"},
+        # traffic and mfma_util_pct are read from the rocprofv3 summaries in
+        # profiles/; they describe the kernels being timed only when the
+        # kernel sources are the ones the summaries were measured with.
+        "profiles_match_kernel_sources": None,
         "cpu_baseline": cpu,
         "median_us_per_call": sig(main_run["median_us_per_call"]),
         "also": {k: {kk: (sig(vv) if isinstance(vv, float) else vv)
                      for kk, vv in v.items()} for k, v in runs.items()},
+    }
+    cur = kernel_sources_sha16()
+    out["profiles_match_kernel_sources"] = {
+        "match": profile_sources(TRAFFIC_PROFILE) == cur == profile_sources(MFMA_PROFILE),
+        "kernel_sources_sha16": cur,
+        "traffic_profile_sha16": profile_sources(TRAFFIC_PROFILE),
+        "mfma_profile_sha16": profile_sources(MFMA_PROFILE),
     }
     for k in out["also"]:
         out["also"][k]["hbm_traffic_bytes"] = load_traffic(k)
