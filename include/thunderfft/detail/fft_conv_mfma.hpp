@@ -588,13 +588,13 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
         for (int b = 0; b < 4; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                region[(16 * b + q + 4 * r) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] =
+                region[tpos(b, q + 4 * r, n)] =
                     pack_half2(v[b][r]);
         wave_lds_sync();
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const u32x4 xv = *reinterpret_cast<const u32x4*>(
-                region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+                region + tchunk(b, n, q));
             dft16_block(op, as_f16x8(xv), v[b]);
         }
     };
@@ -841,13 +841,13 @@ conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict_
         for (int b = 0; b < 4; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                region[(16 * b + q + 4 * r) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] =
+                region[tpos(b, q + 4 * r, n)] =
                     pack_half2(v[b][r]);
         wave_lds_sync();
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const u32x4 xv = *reinterpret_cast<const u32x4*>(
-                region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+                region + tchunk(b, n, q));
             dft16_block(op, as_f16x8(xv), v[b]);
         }
     };

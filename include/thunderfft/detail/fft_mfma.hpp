@@ -129,6 +129,22 @@ __device__ __forceinline__ cpx unpack_half2(unsigned w) {
 
 __device__ __forceinline__ f16x8 as_f16x8(u32x4 w) { return __builtin_bit_cast(f16x8, w); }
 
+// Wave-local transpose between two DFT16 stages (dwords = half2 values):
+// element i of sequence s of block b sits in 16-byte chunk 16 (i >> 2) +
+// (s ^ 2 (i >> 2)) of the block's 64, at slot i & 3.  The reader lane (n, q)
+// takes chunk q of sequence n (its inputs 4 q ... 4 q + 3): the 16 lanes of
+// one q read the 16 chunks of one 256-byte row in XOR-permuted order, which
+// measured conflict-free on MI355X (chunks 4 apart, as a row-per-sequence
+// layout puts them, measured 2-way).  The writer lane (n, q) puts element n
+// of sequence q + 4 r: over each 32-lane half the dword banks differ.
+__device__ __forceinline__ int tpos(int b, int s, int i) {
+    const int g = i >> 2;
+    return 256 * b + 4 * ((s & 12) ^ (4 * (g >> 1))) + (64 * g + 4 * ((s & 3) ^ (2 * (g & 1))) + (i & 3));
+}
+__device__ __forceinline__ int tchunk(int b, int s, int g) {
+    return 256 * b + 4 * (16 * g + (s ^ (2 * g)));
+}
+
 // Plan of the MFMA kernel for N = 256*C = 16 x (C x 16), C in {1, 2, 4, 8}.
 template <int C>
 struct MfmaPlan {
@@ -335,23 +351,22 @@ __device__ __forceinline__ void mfma_steps2to6_w(unsigned* region, W1 w1, const 
 #pragma unroll
             for (int m = 1; m < C; ++m) y[f * C + m][r] = S3::kTwiddle ? s3.twiddle(m, v[m]) : v[m];
         }
-    // ---- step 5: transpose: row 16b + k1 holds the 16 inputs n of
-    // sequence (k1, m) of block b = (f, m); its 4-value chunks are rotated
-    // by k1/4 so reads and writes are bank-conflict free ----
+    // ---- step 5: transpose: sequence (k1, m) of block b = (f, m) gets its
+    // 16 inputs n (tpos: conflict-free writes and 16-byte reads) ----
     wave_lds_sync();
 #pragma unroll
     for (int b = 0; b < kB; ++b)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int k1 = q + 4 * r;
-            region[(16 * b + k1) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] = pack_half2(y[b][r]);
+            region[tpos(b, k1, n)] = pack_half2(y[b][r]);
         }
     wave_lds_sync();
     // ---- step 6: DFT16 over n ----
 #pragma unroll
     for (int b = 0; b < kB; ++b) {
         const u32x4 x = *reinterpret_cast<const u32x4*>(
-            region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+            region + tchunk(b, n, q));
         f16x8 op[2];
         s3.operands(b % C, op);
         dft16_block(op, as_f16x8(x), y[b]);
@@ -720,12 +735,12 @@ __device__ __forceinline__ void mfma4096_fft_regs(unsigned* xbuf, const Mfma4096
     for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            region[(16 * b + q + 4 * r) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] = pack_half2(v[b][r]);
+            region[tpos(b, q + 4 * r, n)] = pack_half2(v[b][r]);
     wave_lds_sync();
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
         const u32x4 xv = *reinterpret_cast<const u32x4*>(
-            region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+            region + tchunk(b, n, q));
         dft16_block(k.a, as_f16x8(xv), v[b]);
     }
 }
@@ -827,22 +842,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void c
 #pragma unroll
             for (int r = 0; r < 4; ++r) y[b][r] = cmul(y[b][r], w2[r]);
         }
-        // ---- wave-local transpose: row 16 b + k2 holds the 16 t0 of (k1, k2) ----
+        // ---- wave-local transpose: sequence (b, k2) gets its 16 t0 (tpos) ----
         wave_lds_sync();
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int k2 = q + 4 * r;
-                region[(16 * b + k2) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] =
-                    pack_half2(y[b][r]);
+                region[tpos(b, k2, n)] = pack_half2(y[b][r]);
             }
         wave_lds_sync();
         // ---- stage 3: DFT16 over t0 -> X[k1 + 16 k2 + 256 k3], k2 = n, k3 = q + 4 r ----
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const u32x4 x = *reinterpret_cast<const u32x4*>(
-                region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+                region + tchunk(b, n, q));
             dft16_block(a, as_f16x8(x), y[b]);
         }
         __half2* dst = out + tile * N;
@@ -1028,21 +1042,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void c
 #pragma unroll
             for (int r = 0; r < 4; ++r) y[b][r] = cmul(y[b][r], w2[r]);
         }
-        // ---- wave-local transpose: row 16 b + k2 holds the 16 t0 of (k1, k2) ----
+        // ---- wave-local transpose: sequence (b, k2) gets its 16 t0 (tpos) ----
         wave_lds_sync();
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int k2 = q + 4 * r;
-                region[(16 * b + k2) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] = pack_half2(y[b][r]);
+                region[tpos(b, k2, n)] = pack_half2(y[b][r]);
             }
         wave_lds_sync();
         // ---- stage 3: DFT16 over t0 -> X_f[k1 + 8 k2 + 128 k3], k2 = n, k3 = q + 4 r ----
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const u32x4 x = *reinterpret_cast<const u32x4*>(
-                region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+                region + tchunk(b, n, q));
             dft16_block(a, as_f16x8(x), y[b]);
         }
         // ---- output: chunk K = (f' 2048 + 4 (w & 1) + 8 n + 128 k3) / 4 of the
@@ -1165,12 +1179,12 @@ __device__ __forceinline__ void mfma2048_fft_regs(unsigned* xbuf, const Mfma2048
     for (int b = 0; b < 4; ++b)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            region[(16 * b + q + 4 * r) * 16 + 4 * (((n >> 2) + r) & 3) + (n & 3)] = pack_half2(v[b][r]);
+            region[tpos(b, q + 4 * r, n)] = pack_half2(v[b][r]);
     wave_lds_sync();
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
         const u32x4 xv = *reinterpret_cast<const u32x4*>(
-            region + (16 * b + n) * 16 + 4 * ((q + (n >> 2)) & 3));
+            region + tchunk(b, n, q));
         dft16_block(k.a, as_f16x8(xv), v[b]);
     }
 }

@@ -52,6 +52,11 @@ inline Grid make_grid(long long ntiles, int per_cu, int num_cus) {
 //   fp16 N = 128 (MFMA, c2c_mfma128_kernel): 2 per CU with prefetch 87.3 us,
 //     against 90.0 at 3 per CU, 99.5 with one tile per workgroup and 90.3-91.1
 //     for the VALU kernel (one tile per workgroup; device grids 93).
+//   fp16 N = 256: one tile per workgroup, 86.0-88.7 us wherever the output
+//     lies; the 2-per-CU grid-stride walk with prefetch is as fast only for
+//     some output placements (86.3-103 us over 12 offsets of y from x, one
+//     box; N = 128, 512, 1024 keep the walk: one tile per workgroup took
+//     98-114 us for them, the per-tile table set-up included).
 //   fp16 MFMA: 2 per CU with prefetch, 86-91 us.  Runs
 //     of contiguous tiles per workgroup, which leave the balancing to the
 //     dispatcher, are slower: 2 tiles 87-98 us, 4-32 tiles 93-110 us (the
@@ -73,7 +78,7 @@ constexpr LaunchShape launch_shape(int precision) {
         return N <= 1024 ? LaunchShape{0, false, N == 256 || N == 512}
                          : LaunchShape{16, true, true};
     if (N == 128) return {2, true};
-    if (N <= 128) return {0, false};
+    if (N <= 128 || N == 256) return {0, false};
     return {2, true};
 }
 
