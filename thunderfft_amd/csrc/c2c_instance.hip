@@ -461,7 +461,13 @@ hipError_t launch_conv2d_cols(int precision, bool conv, const void* in, void* ou
     // wave, no prefetch: 358 us, 124 bytes of spill); half 16 columns 253 us
     // against 277 us with 8 columns (32-byte pieces: a wave's loads then touch
     // twice the rows); one column per wave on MFMA with 16-byte pieces (4
-    // columns per 256-lane workgroup) 545 us.
+    // columns per 256-lane workgroup) 545 us.  A pass over fewer units than
+    // two per CU (one or a few images, and the filter's column pass of every
+    // call) runs 4-column units instead, 256-lane workgroups of one column
+    // per wave, so that more CUs share the columns: one image end to end
+    // (filter spectrum included) fp16 43.5 against 60.8 us, fp32 48.6 against
+    // 52.4 us (2-column fp32 units: 57.5 us); 32 images fp16 248.5 against
+    // 253.1 us (the filter's pass).
     auto launch = [&](auto cols_tag, const void* src, void* dst) {
         constexpr int kCols = decltype(cols_tag)::value;
         constexpr int kPerCu = kColsWavesPerEU<kCols> * 4 / (kColsLanes<kCols> / 64);
@@ -487,7 +493,10 @@ hipError_t launch_conv2d_cols(int precision, bool conv, const void* in, void* ou
                     static_cast<const __half2*>(src), static_cast<float2*>(dst), H, units, scale, tw);
         }
     };
-    if (precision == 0)
+    const long long wide = precision == 0 ? 8 : 16;
+    if (images * (cols / wide) < 2LL * (num_cus > 0 ? num_cus : 256))
+        launch(std::integral_constant<int, 4>{}, in, out);
+    else if (precision == 0)
         launch(std::integral_constant<int, 8>{}, in, out);
     else
         launch(std::integral_constant<int, 16>{}, in, out);
