@@ -15,7 +15,10 @@ transient after a pause), then K steps back to back between two HIP events
 recorded on the launch stream, bracketed by device synchronisation;
 ms_per_step is the event time / K.  value = GFLOP/s (5 N log2 N per
 transform) of the float forward transform; the inverse and the half
-transforms are measured the same way and reported under "also".
+transforms are measured the same way and reported under "also".  Each leg
+allocates its output right after its input; also.placement_*_n1024 repeats
+the forward transform with the output at 8 offsets inside one allocation,
+since the fp16 kernels' time depends on where the output lies.
 
 roofline.achieved = algorithmic bytes per launch (read + write of every
 complex value once: 2 * batch * N * sizeof(T)) / the mean launch duration
@@ -317,6 +320,41 @@ COMPUTE_KERNELS = {
     "float_mfma_f32": "fp32 data, both DFT16 stages on v_mfma_f32_16x16x4_f32",
     "float_mfma_bf16x3": "fp32 data, both DFT16 stages as bf16x3 on v_mfma_f32_16x16x32_bf16",
 }
+
+
+def placement_spread(T: str, steps: int, warmup: int,
+                     offsets_mib=(0, 32, 64, 96, 128, 160, 192, 224)) -> dict:
+    """The C2C of the main workload (N=1024 x 65536 forward) with its output
+    placed at x + (buffer size) + d MiB inside one allocation, for each d in
+    offsets_mib.  On MI355X the fp16 MFMA kernels' time depends on where the
+    output lies relative to the input (a pattern repeating every 128 MiB of d,
+    and differing between processes for the same d: the physical pages
+    differ); the fp32 kernel's does not.  The spread bounds what a single
+    placement, such as the other legs', can read."""
+    import torch
+
+    import thunderfft_amd as thff
+
+    n, batch = N_FFT, BATCH
+    dt = torch.float32 if T == "float" else torch.float16
+    esize = 4 if T == "float" else 2            # bytes per real component
+    per_mib = (1 << 20) // esize                # components per MiB
+    comps = 2 * n * batch                       # components per buffer
+    big = torch.empty(2 * comps + max(offsets_mib) * per_mib, dtype=dt, device="cuda")
+    x = big[:comps]
+    stream = torch.cuda.current_stream()
+    thff.fill_uniform(T, x, n * batch, 0x7F4A7C15 + n, 0, stream)
+    thff.ThunderFFTInitialize(T, n)
+    us = []
+    for d in offsets_mib:
+        y = big[comps + d * per_mib: 2 * comps + d * per_mib]
+        ms = timed(lambda: thff.ThunderFFT_global_async(T, n, True, x, y, batch, stream),
+                   steps, warmup, stream)
+        us.append(round(ms * 1e3, 2))
+    del big, x
+    return {"workload": f"C2C {T}2 forward N={n} x {batch}, output at x + {comps * esize >> 20} "
+                        f"MiB + d", "offsets_mib": list(offsets_mib), "us_per_call": us,
+            "min_us": min(us), "median_us": statistics.median(us), "max_us": max(us)}
 
 
 def compute_differential(T: str, repeats: int = 1000, trials: int = 3) -> dict:
@@ -718,6 +756,11 @@ def main():
         runs[f"sync_wrapper_{T}_fwd"] = r
         print(f"[bench] {T} N=1024 x 65536 synchronous ThunderFFT_global: "
               f"{r['median_us_per_call']:.1f} us per call (median of {r['calls']})",
+              file=sys.stderr, flush=True)
+    for T in ("float", "half"):
+        r = placement_spread(T, max(5, a.steps // 4), max(1, a.warmup // 4))
+        runs[f"placement_{T}_n1024"] = r
+        print(f"[bench] {r['workload']}, d = {r['offsets_mib']} MiB: {r['us_per_call']} us",
               file=sys.stderr, flush=True)
     thff.ThunderFFTFinalize("float")
     thff.ThunderFFTFinalize("half")
