@@ -257,22 +257,22 @@ struct Stage3Plain {
 // w1 = [c][r][lane], and for the stage before the last DFT16 either the
 // folded operands a3 (Stage3Folded; a3 non-null) or this lane's twiddles
 // w2[m - 1] = W_16C^(n m) (Stage3Plain; w2 non-null).  Collective over the
-// 256-lane workgroup (ends with a barrier).
-template <int C, bool FWD>
+// kThreads-lane workgroup (ends with a barrier).
+template <int C, bool FWD, int kThreads = 256>
 __device__ __forceinline__ void mfma_setup(f16x8 (&a)[2], cpx* w1, u32x4* a3, cpx* w2,
                                            const float2* __restrict__ tw) {
     using P = MfmaPlan<C>;
     constexpr int N = P::N;
     const int tid = threadIdx.x, lane = tid & 63, n = lane & 15;
     dft16_operands<FWD>(a, lane);
-    for (int e = tid; e < P::kTw1; e += 256) {
+    for (int e = tid; e < P::kTw1; e += kThreads) {
         const int l = e & 63, r = (e >> 6) & 3, c = e >> 8;
         const float2 x = tw[((16 * c + (l & 15)) * ((l >> 4) + 4 * r)) & (N - 1)];
         w1[e] = FWD ? cpx{x.x, -x.y} : cpx{x.x, x.y};
     }
     if constexpr (C > 1) {
         if (a3) {
-            for (int e = tid; e < (C - 1) * 2 * 64; e += 256) {
+            for (int e = tid; e < (C - 1) * 2 * 64; e += kThreads) {
                 const int l = e & 63, h = (e >> 6) & 1, m = 1 + (e >> 7);
                 a3[e] = __builtin_bit_cast(u32x4, dft16_operand_twiddled<FWD>(l, h, m, C, tw));
             }
