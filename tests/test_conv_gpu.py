@@ -382,11 +382,13 @@ def test_conv2d_large_images_match_direct_convolution(T, size):
 
 
 @pytest.mark.parametrize("T", ["float", "half"])
-@pytest.mark.parametrize("size,batch", [(128, 2048 + 3), (1024, 32)])
+@pytest.mark.parametrize("size,batch", [(128, 2048 + 3), (1024, 32), (1024, 9)])
 def test_conv2d_large_image_batches(T, size, batch):
     """Benchmark-sized batches (2^25 values, plus a few images so the walk is
-    uneven at 128): a subset of images against the direct convolution with the
-    7 x 7 corner filter, then a one-tap filter rolls every image."""
+    uneven at 128), and 9 images at 1024 (the half2 column pass on MFMA with
+    an uneven grid-stride walk): a subset of images against the direct
+    convolution with the 7 x 7 corner filter, then a one-tap filter rolls
+    every image."""
     import torch
 
     import thunderfft_amd as thff
