@@ -46,6 +46,8 @@ def lib():
         L.thff_fft_f64.argtypes = [ctypes.c_int, ctypes.c_long, ctypes.c_int, dp, dp]
         L.thff_fft_f32_fourstep.argtypes = [ctypes.c_int, ctypes.c_long, ctypes.c_int, fp, fp,
                                             ctypes.c_int]
+        L.thff_fft_f32_batched.argtypes = [ctypes.c_int, ctypes.c_long, ctypes.c_int, fp, fp,
+                                           ctypes.c_int]
         L.thff_metrics.argtypes = [ctypes.c_long, fp, dp, dp]
         L.thff_metrics.restype = None
         L.thff_f32_to_f16_array.argtypes = [ctypes.c_long, fp, u16p]
@@ -114,6 +116,23 @@ def fft_f32_fourstep(x, forward: bool = True, threads: int = 1) -> np.ndarray:
                                        _p(x.view(np.float32), ctypes.c_float),
                                        _p(out.view(np.float32), ctypes.c_float), threads),
            "fft_f32_fourstep")
+    return out
+
+
+def fft_f32_batched(x, forward: bool = True, threads: int = 1, out=None) -> np.ndarray:
+    """fp32 radix-4 FFT vectorised across 16 signals at a time (the CPU
+    baseline; thff_oracle_simd.c).  `out`: a complex64 array of x's shape to
+    write into (reused by a timing loop, so no pass pays for new pages)."""
+    x = np.ascontiguousarray(x, dtype=np.complex64)
+    n = x.shape[-1]
+    if out is None:
+        out = np.empty_like(x)
+    if out.shape != x.shape or out.dtype != np.complex64 or not out.flags.c_contiguous:
+        raise ValueError("out must be a C-contiguous complex64 array of x's shape")
+    _check(lib().thff_fft_f32_batched(n, x.size // n, -1 if forward else 1,
+                                      _p(x.view(np.float32), ctypes.c_float),
+                                      _p(out.view(np.float32), ctypes.c_float), threads),
+           "fft_f32_batched")
     return out
 
 

@@ -172,6 +172,38 @@ def test_fourstep_threads_bitwise_identical():
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
+# ---------------------------------------------------------------- fp32 batched baseline
+@pytest.mark.parametrize("n", SIZES)
+def test_batched_f32_accuracy(n):
+    """The CPU baseline's 16-signal vector groups, on a batch that is not a
+    multiple of 16 (the last group padded), against the fp64 FFT."""
+    x = oracle.uniform(n, 37)
+    for forward in (True, False):
+        got = oracle.fft_f32_batched(x, forward, threads=3)
+        m = oracle.metrics(got, oracle.fft(x, forward))
+        assert m["rel_l2"] < 1e-6 and m["nonfinite"] == 0
+
+
+def test_batched_f32_kats_and_threads():
+    """Closed forms (an offset impulse's phasor, a tone's single bin) and a
+    result independent of the thread count; a reused output is overwritten."""
+    n, b = 256, 20
+    x = np.zeros((b, n), np.complex64)
+    x[:, 5] = 0.75 + 0.25j
+    got = oracle.fft_f32_batched(x, True)
+    k = np.arange(n)
+    want = (0.75 + 0.25j) * np.exp(-2j * np.pi * k * 5 / n)
+    assert np.max(np.abs(got - want)) < 1e-6
+    t = np.exp(2j * np.pi * 7 * k / n).astype(np.complex64)
+    got = oracle.fft_f32_batched(np.tile(t, (b, 1)), True)
+    assert abs(got[3, 7] - n) < 1e-3 and np.max(np.abs(np.delete(got[3], 7))) < 1e-3
+    y = oracle.uniform(1024, 53)
+    out = np.full(y.shape, np.nan, np.complex64)
+    a = oracle.fft_f32_batched(y, True, threads=1)
+    c = oracle.fft_f32_batched(y, True, threads=7, out=out)
+    assert c is out and np.array_equal(a.view(np.uint32), c.view(np.uint32))
+
+
 # ---------------------------------------------------------------- half rounding
 def test_f16_conversion_matches_numpy():
     rng = np.random.default_rng(3)
