@@ -22,14 +22,22 @@
 
 namespace thff {
 
+// Two dwords of half values -> one: {s1.lo, s0.lo} (kHalvesLow) or {s1.hi,
+// s0.hi} (kHalvesHigh), one v_perm_b32 (selector bytes 0-3 pick bytes of s1,
+// 4-7 bytes of s0) instead of a mask, a shift and an or.
+inline constexpr unsigned kHalvesLow = 0x05040100u, kHalvesHigh = 0x07060302u;
+__device__ __forceinline__ unsigned halves(unsigned s0, unsigned s1, unsigned sel) {
+    return __builtin_amdgcn_perm(s0, s1, sel);
+}
+
 // Two rows of halves (8 per 16-byte word) <-> 8 half2 (row 0 = real part).
 __device__ __forceinline__ void interleave_rows(u32x4 r0, u32x4 r1, u32x4& lo, u32x4& hi) {
     const unsigned a[4] = {r0.x, r0.y, r0.z, r0.w}, b[4] = {r1.x, r1.y, r1.z, r1.w};
     unsigned z[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        z[2 * i] = (a[i] & 0xffffu) | (b[i] << 16);
-        z[2 * i + 1] = (a[i] >> 16) | (b[i] & 0xffff0000u);
+        z[2 * i] = halves(b[i], a[i], kHalvesLow);
+        z[2 * i + 1] = halves(b[i], a[i], kHalvesHigh);
     }
     lo = u32x4{z[0], z[1], z[2], z[3]};
     hi = u32x4{z[4], z[5], z[6], z[7]};
@@ -39,8 +47,8 @@ __device__ __forceinline__ void split_rows(u32x4 lo, u32x4 hi, u32x4& r0, u32x4&
     unsigned a[4], b[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        a[i] = (z[2 * i] & 0xffffu) | (z[2 * i + 1] << 16);
-        b[i] = (z[2 * i] >> 16) | (z[2 * i + 1] & 0xffff0000u);
+        a[i] = halves(z[2 * i + 1], z[2 * i], kHalvesLow);
+        b[i] = halves(z[2 * i + 1], z[2 * i], kHalvesHigh);
     }
     r0 = u32x4{a[0], a[1], a[2], a[3]};
     r1 = u32x4{b[0], b[1], b[2], b[3]};
@@ -469,13 +477,22 @@ namespace thff {
 //            two rows: 4 consecutive values of each, interleaved into half2),
 //            exchange, stage 2, transpose, stage 3 -> lane (n, q) of block b
 //            holds Z[k1 + 16 k2 + 256 k3], k1 = 4 w + b, k2 = n, k3 = q + 4 r;
-//   product with the channel's spectrum;
-//   inverse: stage 1 straight from those registers (sequence t' = k1 + 16 k2
+//   product with the channel's spectrum, conjugated;
+//   inverse: as conj(DFT(conj(Z H))), the same forward stages: stage 1
+//            straight from those registers (sequence t' = k1 + 16 k2
 //            = 4 w + b + 16 n, inputs k3 = q + 4 r: interleaved operands),
 //            exchange with t0' = 4 w + b, t1' = n, stage 2, transpose,
-//            stage 3 -> y[k1' + 16 k2' + 256 k3'], then staged output split
-//            back into the two rows.
-// The exchange layout is xaddr4096 (fft_mfma.hpp).
+//            stage 3 -> conj(y[k1' + 16 k2' + 256 k3']), then staged output
+//            (conjugated back) split into the two rows.
+// The exchange layout is xaddr4096 (fft_mfma.hpp).  The stage-1 -> 2 twiddle
+// W^(t k1) is not multiplied in: with t = t0 + 16 t1 it is W_256^(t1 k1)
+// W_4096^(t0 k1); the exchange gives each stage-2 block one k1 (its inputs
+// t1, its sequences t0), so the first factor is folded into that block's
+// operand columns (dft16_operand_twiddled) and the second into the stage-2 ->
+// 3 twiddle.  Against the fp32 multiply after stage 1 (and the inverse's own
+// operands, and the interleave by shifts and masks instead of v_perm_b32):
+// 62.0-64.6 against 73.9-76.5 us for 2^26 samples, per-tile VALU 499 -> 360
+// instructions, rel L2 against fp64 5.99e-4 against 6.14e-4 (MI355X).
 // Every HBM access is 16 bytes: lanes n and n + 1 (n even) need the same 8
 // consecutive values of both rows (4 each), so the even lane loads row 0's 8,
 // the odd lane row 1's, and they swap the halves the other needs (a DPP lane
@@ -541,27 +558,31 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
     const int n = lane & 15, q = lane >> 4;
     unsigned* const region = xbuf + 4 * P::kMatrix * wave;
 
-    f16x8 a[2], ai[2], ai_regs[2];
+    // Both directions run the forward transform: the inverse is
+    // conj(DFT(conj(P))), its input conjugated at the product and its output
+    // at the store.  Operands: `a` plain (forward stage 1, stage 3),
+    // `a_regs` column-permuted (the inverse's stage 1 from registers), and
+    // per block b the stage-2 matrix of k1 = 4 w + b with the stage-1 -> 2
+    // twiddle's factor W_256^(t1 k1) folded into its columns (the exchange
+    // gives every block one k1: its 16 sequences are t0 = n, its inputs t1).
+    // The rest of that twiddle, W_4096^(t0 k1), joins the stage-2 -> 3
+    // twiddle W_256^(t0 k2): w2[b][r] = W^(n (k1 + 16 k2)), k2 = q + 4 r
+    // (positive angles, conjugated at use).  No multiply remains between
+    // stages 1 and 2; the folded factor is rounded into the f16 coefficient,
+    // the size of the f16 rounding of the data at that stage.
+    f16x8 a[2], a_regs[2], a2[4][2];
     dft16_operands<true>(a, lane);
-    dft16_operands<false>(ai, lane);
-    dft16_operands<false, true>(ai_regs, lane);
-    // Twiddles (positive angles; the forward conjugates): stage 1 -> 2
-    // W^(t k1) for the forward's t = 64 w + 4 n + b and the inverse's
-    // t' = 4 w + b + 16 n; stage 2 -> 3 W^(16 n k2), k = q + 4 r.
-    cpx w1f[4][4], w1i[4][4], w2[4];
+    dft16_operands<true, true>(a_regs, lane);
+    cpx w2[4][4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < 4; ++b) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) a2[b][h] = dft16_operand_twiddled<true>(lane, h, 4 * wave + b, 16, tw);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float2 f = tw[((64 * wave + 4 * n + b) * (q + 4 * r)) & (N - 1)];
-            const float2 g = tw[((4 * wave + b + 16 * n) * (q + 4 * r)) & (N - 1)];
-            w1f[b][r] = cpx{f.x, -f.y};
-            w1i[b][r] = cpx{g.x, g.y};
+            const float2 g = tw[(n * (4 * wave + b + 16 * (q + 4 * r))) & (N - 1)];
+            w2[b][r] = cpx{g.x, g.y};
         }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const float2 g = tw[(16 * n * (q + 4 * r)) & (N - 1)];
-        w2[r] = cpx{g.x, g.y};
     }
 
     // tiles_per_block = 0: the grid is sized to the device and walks the
@@ -570,8 +591,8 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
     long long tile, tile_end, step;
     tile_walk(transforms, tiles_per_block, tile, tile_end, step);
 
-    // Stage 2 of either direction, the wave-local transpose and stage 3.
-    auto stages23 = [&](cpx (&v)[4][4], const f16x8 (&op)[2], bool conj_w2) {
+    // Stage 2 (twiddle-folded operands), the wave-local transpose and stage 3.
+    auto stages23 = [&](cpx (&v)[4][4]) {
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const u32x4 raw = *reinterpret_cast<const u32x4*>(
@@ -579,9 +600,9 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
             u32x4 xv;  // t1 = 4 q + e sits at position (e + k1) & 3 = (e + b) & 3
 #pragma unroll
             for (int e = 0; e < 4; ++e) xv[e] = raw[(e + b) & 3];
-            dft16_block(op, as_f16x8(xv), v[b]);
+            dft16_block(a2[b], as_f16x8(xv), v[b]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[b][r] = conj_w2 ? cmulc(v[b][r], w2[r]) : cmul(v[b][r], w2[r]);
+            for (int r = 0; r < 4; ++r) v[b][r] = cmulc(v[b][r], w2[b][r]);
         }
         wave_lds_sync();
 #pragma unroll
@@ -595,7 +616,7 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
         for (int b = 0; b < 4; ++b) {
             const u32x4 xv = *reinterpret_cast<const u32x4*>(
                 region + tchunk(b, n, q));
-            dft16_block(op, as_f16x8(xv), v[b]);
+            dft16_block(a, as_f16x8(xv), v[b]);
         }
     };
 
@@ -607,6 +628,14 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
     const ChannelWalk walk(step, channels);  // pair and channel of the tile, advanced per tile
     ChannelPos pos = walk.at(tile);
     const bool odd = (lane & 1) != 0;
+    // Byte selectors of v_perm_b32 (halves): kLow {s1.lo, s0.lo}, kHigh
+    // {s1.hi, s0.hi}, and the other order.  Per lane they put row 0's value
+    // in the low half of each half2.
+    constexpr unsigned kLow = kHalvesLow, kHigh = kHalvesHigh;
+    constexpr unsigned kLowSwapped = 0x01000504u, kHighSwapped = 0x03020706u;
+    const unsigned sel_lo = odd ? kLowSwapped : kLow, sel_hi = odd ? kHighSwapped : kHigh;
+    // Output: a row's two values out of two half2 dwords: row 0 (kLow) or row 1 (kHigh).
+    const unsigned sel_keep = odd ? kHigh : kLow, sel_send = odd ? kLow : kHigh;
     // Element offsets of a tile's two rows (row 1: -1 past an odd batch's end).
     auto rows = [&](ChannelPos ps, long long& r0, long long& r1) {
         r0 = (2 * ps.p * channels + ps.d) * N;
@@ -670,13 +699,13 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const u32x4 w = next[e];
-            // even lane: keeps row 0's first half, gets row 1's; odd: the reverse
+            // even lane: keeps row 0's first half (u), gets row 1's (g);
+            // odd: keeps row 1's second half, gets row 0's
+            const unsigned u0 = odd ? w.z : w.x, u1 = odd ? w.w : w.y;
             const unsigned g0 = swap_lane_pair(odd ? w.x : w.z);
             const unsigned g1 = swap_lane_pair(odd ? w.y : w.w);
-            const u32x2 a0 = odd ? u32x2{g0, g1} : u32x2{w.x, w.y};
-            const u32x2 a1 = odd ? u32x2{w.z, w.w} : u32x2{g0, g1};
-            z[e] = u32x4{(a0.x & 0xffffu) | (a1.x << 16), (a0.x >> 16) | (a1.x & 0xffff0000u),
-                         (a0.y & 0xffffu) | (a1.y << 16), (a0.y >> 16) | (a1.y & 0xffff0000u)};
+            z[e] = u32x4{halves(g0, u0, sel_lo), halves(g0, u0, sel_hi),
+                         halves(g1, u1, sel_lo), halves(g1, u1, sel_hi)};
         }
         if constexpr (kBufferIO)
             load(pos, next, tile + step < tile_end);
@@ -689,8 +718,6 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
 #pragma unroll
             for (int e = 0; e < 4; ++e) xv[e] = z[e][b];
             dft16_block(a, as_f16x8(xv), v[b]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], w1f[b][r]);
         }
         __syncthreads();  // every wave is done with the previous tile's exchange buffer
 #pragma unroll
@@ -699,7 +726,7 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
             for (int r = 0; r < 4; ++r)
                 xbuf[xaddr4096(q + 4 * r, 4 * (n & 3) + b, 4 * wave + (n >> 2))] = pack_half2(v[b][r]);
         __syncthreads();
-        stages23(v, a, true);
+        stages23(v);
         // ---- product: bin k = 4 w + b + 16 n + 256 (q + 4 r) ----
         if (d != spec_d) {  // uniform: a new channel's spectrum
             const float2* hs = spectrum + d * N + 4 * wave + 16 * n + 256 * q;
@@ -708,7 +735,7 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float2 hk = hs[b + 1024 * r];
-                    spec[b][r] = cpx{hk.x, hk.y};
+                    spec[b][r] = cpx{hk.x, -hk.y};  // conj(H)
                 }
             // Wait here, on this rarely taken path: a wait after the branch
             // would have to count these loads as the latest ones and so
@@ -716,19 +743,19 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
             wait_vmem_all();
             spec_d = d;
         }
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], spec[b][r]);
-        // ---- inverse stage 1 from the registers, then W^(t' k1') ----
+        // ---- inverse stage 1 from the registers: the forward DFT16 over k3
+        // of conj(Z H) = conj(Z conj(G)), G = conj(H) held in spec, sequences
+        // t' = 4 w + b + 16 n (written as two products each, which the
+        // compiler fuses with the f16 rounding) ----
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             u32x4 xv;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) xv[r] = pack_half2(v[b][r]);
-            dft16_block(ai_regs, as_f16x8(xv), v[b]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], w1i[b][r]);
+            for (int r = 0; r < 4; ++r) {
+                const cpx z = v[b][r], g = spec[b][r];
+                xv[r] = pack_half2(cpx{z.re * g.re + z.im * g.im, z.re * g.im - z.im * g.re});
+            }
+            dft16_block(a_regs, as_f16x8(xv), v[b]);
         }
         __syncthreads();  // every wave's forward stage-3 reads are done
 #pragma unroll
@@ -737,34 +764,35 @@ conv1d_real_mfma4096_kernel(const __half* __restrict__ x, const float2* __restri
             for (int r = 0; r < 4; ++r)
                 xbuf[xaddr4096(q + 4 * r, 4 * wave + b, n)] = pack_half2(v[b][r]);
         __syncthreads();
-        stages23(v, ai, false);
-        // ---- output: y[k1 + 16 k2 + 256 k3], k1 = 4 w + b, k2 = n, k3 = q + 4 r ----
+        stages23(v);
+        // ---- output: conj of the forward result is y[k1 + 16 k2 + 256 k3],
+        // k1 = 4 w + b, k2 = n, k3 = q + 4 r ----
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             reinterpret_cast<u32x4*>(obuf)[P::out_chunk(wave + 4 * n + 64 * (q + 4 * r))] =
-                u32x4{pack_half2(v[0][r]), pack_half2(v[1][r]), pack_half2(v[2][r]),
-                      pack_half2(v[3][r])};
+                u32x4{pack_half2(cpx{v[0][r].re, -v[0][r].im}), pack_half2(cpx{v[1][r].re, -v[1][r].im}),
+                      pack_half2(cpx{v[2][r].re, -v[2][r].im}), pack_half2(cpx{v[3][r].re, -v[3][r].im})};
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int k = 4 * tid + 1024 * i;
             const u32x4 z4 = reinterpret_cast<const u32x4*>(obuf)[P::out_chunk(tid + 256 * i)];
-            const unsigned zz[4] = {z4.x, z4.y, z4.z, z4.w};
-            const u32x2 o0{(zz[0] & 0xffffu) | (zz[1] << 16), (zz[2] & 0xffffu) | (zz[3] << 16)};
-            const u32x2 o1{(zz[0] >> 16) | (zz[1] & 0xffff0000u), (zz[2] >> 16) | (zz[3] & 0xffff0000u)};
             // values k .. k + 3 of both rows; the even lane stores row 0's
-            // k .. k + 7, the odd lane row 1's k - 4 .. k + 3
-            const unsigned g0 = swap_lane_pair(odd ? o0.x : o1.x);
-            const unsigned g1 = swap_lane_pair(odd ? o0.y : o1.y);
+            // k .. k + 7, the odd lane row 1's k - 4 .. k + 3: each keeps
+            // its own row's four values and sends the other row's
+            const u32x2 keep{halves(z4.y, z4.x, sel_keep),
+                             halves(z4.w, z4.z, sel_keep)};
+            const unsigned g0 = swap_lane_pair(halves(z4.y, z4.x, sel_send));
+            const unsigned g1 = swap_lane_pair(halves(z4.w, z4.z, sel_send));
             if constexpr (kBufferIO) {
-                const u32x4 w4 = odd ? u32x4{g0, g1, o1.x, o1.y} : u32x4{o0.x, o0.y, g0, g1};
+                const u32x4 w4 = odd ? u32x4{g0, g1, keep.x, keep.y} : u32x4{keep.x, keep.y, g0, g1};
                 __builtin_amdgcn_raw_buffer_store_b128(w4, yrs, real4096_store_offset(channels, tid, i),
                                                        0, 2);
             } else {
                 if (!odd)
-                    st_nt(reinterpret_cast<u32x4*>(y + row0 + k), u32x4{o0.x, o0.y, g0, g1});
+                    st_nt(reinterpret_cast<u32x4*>(y + row0 + k), u32x4{keep.x, keep.y, g0, g1});
                 else if (row1 >= 0)
-                    st_nt(reinterpret_cast<u32x4*>(y + row1 + k - 4), u32x4{g0, g1, o1.x, o1.y});
+                    st_nt(reinterpret_cast<u32x4*>(y + row1 + k - 4), u32x4{g0, g1, keep.x, keep.y});
             }
         }
     }
@@ -781,12 +809,16 @@ namespace thff {
 // filter spectrum kept packed as half2 (1/N folded in) and the inverse from
 // registers, as in conv1d_real_mfma4096_kernel.  Grid: sized to the device
 // (a few workgroups per CU), walking the signals grid-stride (tile_walk).
+// The stage-1 -> 2 twiddle is folded into the stage-2 operands and the
+// stage-2 -> 3 twiddle, and the inverse runs the forward stages on the
+// conjugated product, as there: 89.5-91.2 against 95.5-97.0 us (per-signal
+// filters), 58.2-60.3 against 64.1-66.4 us (shared filter), 2^25 values.
 // Per-signal filters: held to 168 VGPRs (3 workgroups per CU) at the cost of a
-// 32-byte spill, 103 us against 111 us at 2 per CU (2^25 values, MI355X).  A
-// shared filter keeps its spectrum live across the loop: 2 per CU, and the
-// next signal's loads are issued before the current one's transform (64 us
-// against 73 us; for per-signal filters the extra registers spill and it
-// measured slower, 102 against 97 us).
+// 24-byte spill: 89.5-91.2 us against 92.8-93.8 us at 2 per CU (170 VGPRs, no
+// spill; MI355X).  A shared filter keeps its spectrum live across the loop: 2
+// per CU, and the next signal's loads are issued before the current one's
+// transform (64 us against 73 us before the fold; for per-signal filters the
+// extra registers spill and it measured slower, 102 against 97 us).
 template <bool kPerSignal>
 inline constexpr int kConv4096MinWavesPerEU = kPerSignal ? 3 : 2;
 
@@ -804,27 +836,26 @@ conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict_
     unsigned* const region = xbuf + 4 * P::kMatrix * wave;
     constexpr float kScale = 1.0f / N;
 
-    f16x8 a[2], ai[2], ai_regs[2];
+    // As in conv1d_real_mfma4096_kernel: both directions run the forward
+    // transform (the inverse as conj(DFT(conj(P)))), with the stage-1 -> 2
+    // twiddle folded into the per-block stage-2 operands a2 and the
+    // stage-2 -> 3 twiddles w2[b][r] = W^(n (k1 + 16 k2)).
+    f16x8 a[2], a_regs[2], a2[4][2];
     dft16_operands<true>(a, lane);
-    dft16_operands<false>(ai, lane);
-    dft16_operands<false, true>(ai_regs, lane);
-    cpx w1f[4][4], w1i[4][4], w2[4];
+    dft16_operands<true, true>(a_regs, lane);
+    cpx w2[4][4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < 4; ++b) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) a2[b][hh] = dft16_operand_twiddled<true>(lane, hh, 4 * wave + b, 16, tw);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float2 f = tw[((64 * wave + 4 * n + b) * (q + 4 * r)) & (N - 1)];
-            const float2 g = tw[((4 * wave + b + 16 * n) * (q + 4 * r)) & (N - 1)];
-            w1f[b][r] = cpx{f.x, -f.y};
-            w1i[b][r] = cpx{g.x, g.y};
+            const float2 g = tw[(n * (4 * wave + b + 16 * (q + 4 * r))) & (N - 1)];
+            w2[b][r] = cpx{g.x, g.y};
         }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const float2 g = tw[(16 * n * (q + 4 * r)) & (N - 1)];
-        w2[r] = cpx{g.x, g.y};
     }
 
-    auto stages23 = [&](cpx (&v)[4][4], const f16x8 (&op)[2], bool conj_w2) {
+    auto stages23 = [&](cpx (&v)[4][4]) {
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const u32x4 raw = *reinterpret_cast<const u32x4*>(
@@ -832,9 +863,9 @@ conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict_
             u32x4 xv;
 #pragma unroll
             for (int e = 0; e < 4; ++e) xv[e] = raw[(e + b) & 3];
-            dft16_block(op, as_f16x8(xv), v[b]);
+            dft16_block(a2[b], as_f16x8(xv), v[b]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[b][r] = conj_w2 ? cmulc(v[b][r], w2[r]) : cmul(v[b][r], w2[r]);
+            for (int r = 0; r < 4; ++r) v[b][r] = cmulc(v[b][r], w2[b][r]);
         }
         wave_lds_sync();
 #pragma unroll
@@ -848,7 +879,7 @@ conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict_
         for (int b = 0; b < 4; ++b) {
             const u32x4 xv = *reinterpret_cast<const u32x4*>(
                 region + tchunk(b, n, q));
-            dft16_block(op, as_f16x8(xv), v[b]);
+            dft16_block(a, as_f16x8(xv), v[b]);
         }
     };
     // Stage-1 inputs of the 4096 values at src: x[64 w + 4 n + b + 256 j],
@@ -867,8 +898,6 @@ conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict_
 #pragma unroll
             for (int e = 0; e < 4; ++e) xv[e] = z[e][b];
             dft16_block(a, as_f16x8(xv), v[b]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], w1f[b][r]);
         }
         __syncthreads();
 #pragma unroll
@@ -877,15 +906,16 @@ conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict_
             for (int r = 0; r < 4; ++r)
                 xbuf[xaddr4096(q + 4 * r, 4 * (n & 3) + b, 4 * wave + (n >> 2))] = pack_half2(v[b][r]);
         __syncthreads();
-        stages23(v, a, true);
+        stages23(v);
     };
 
-    unsigned hp[4][4];  // FFT(h) / N at bins 4 w + b + 16 n + 256 (q + 4 r), packed half2
+    // conj(FFT(h)) / N at bins 4 w + b + 16 n + 256 (q + 4 r), packed half2
+    unsigned hp[4][4];
     auto keep = [&](const cpx (&v)[4][4]) {
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) hp[b][r] = pack_half2({v[b][r].re * kScale, v[b][r].im * kScale});
+            for (int r = 0; r < 4; ++r) hp[b][r] = pack_half2({v[b][r].re * kScale, -v[b][r].im * kScale});
     };
     long long tile, tile_end, step;
     tile_walk(batch, 0, tile, tile_end, step);
@@ -921,22 +951,19 @@ conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict_
             if (tile + step < tile_end) load(x + (tile + step) * N, zx);
             forward(z, v);
         }
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float2 hk = __half22float2(__builtin_bit_cast(__half2, hp[b][r]));
-                v[b][r] = cmul(v[b][r], cpx{hk.x, hk.y});
-            }
-        // ---- inverse: stage 1 from the registers, exchange, stages 2-3 ----
+        // ---- inverse: the forward DFT16 over k3 of conj(Z H) = conj(Z
+        // conj(G)), G = conj(H) held in hp, from the registers; exchange,
+        // stages 2-3; the output conjugated at the staging ----
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             u32x4 xv;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) xv[r] = pack_half2(v[b][r]);
-            dft16_block(ai_regs, as_f16x8(xv), v[b]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) v[b][r] = cmul(v[b][r], w1i[b][r]);
+            for (int r = 0; r < 4; ++r) {
+                const float2 g = __half22float2(__builtin_bit_cast(__half2, hp[b][r]));
+                const cpx z = v[b][r];
+                xv[r] = pack_half2(cpx{z.re * g.x + z.im * g.y, z.re * g.y - z.im * g.x});
+            }
+            dft16_block(a_regs, as_f16x8(xv), v[b]);
         }
         __syncthreads();
 #pragma unroll
@@ -945,12 +972,12 @@ conv1d_mfma4096_kernel(const __half2* __restrict__ x, const __half2* __restrict_
             for (int r = 0; r < 4; ++r)
                 xbuf[xaddr4096(q + 4 * r, 4 * wave + b, n)] = pack_half2(v[b][r]);
         __syncthreads();
-        stages23(v, ai, false);
+        stages23(v);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             reinterpret_cast<u32x4*>(obuf)[P::out_chunk(wave + 4 * n + 64 * (q + 4 * r))] =
-                u32x4{pack_half2(v[0][r]), pack_half2(v[1][r]), pack_half2(v[2][r]),
-                      pack_half2(v[3][r])};
+                u32x4{pack_half2(cpx{v[0][r].re, -v[0][r].im}), pack_half2(cpx{v[1][r].re, -v[1][r].im}),
+                      pack_half2(cpx{v[2][r].re, -v[2][r].im}), pack_half2(cpx{v[3][r].re, -v[3][r].im})};
         __syncthreads();
         __half2* dst = y + tile * N;
 #pragma unroll
