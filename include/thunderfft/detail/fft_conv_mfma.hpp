@@ -67,6 +67,14 @@ __device__ __forceinline__ void split_rows(u32x4 lo, u32x4 hi, u32x4& r0, u32x4&
 // product reads the channel's spectrum (fp32, L2-resident) per tile.
 template <int C>
 inline constexpr int kConvMfmaMinWavesPerEU = C == 1 || C == 8 ? 2 : 3;
+// At C = 8 (N = 2048) the DFT8 between the two DFT16 stages of the complex
+// fp16 convolution runs on the matrix cores (mfma8_steps2to6_dft8mfma)
+// instead of in-lane: 81.5-82.8 against 84.3-86.8 us for 16384 x 2048
+// per-signal filters, 59.5-60.9 against 62.1-64.3 us with a shared filter,
+// rel L2 against fp64 6.55e-4 against 5.71e-4 (one more f16 rounding,
+// MI355X).  The real convolution at N = 2048 keeps the in-lane DFT8: on the
+// matrix cores it measured 68.5-69.6 against 67.6-69.1 us, with more error.
+inline constexpr bool kConv1dDft8OnMfma = true;
 
 // kBufferIO addressing of conv1d_real_mfma_kernel.  A wave's transforms tau0
 // ... tau0 + kFPW - 1 (pairs p, channels d, consecutive in tau) read and
@@ -316,6 +324,15 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
 #pragma unroll
     for (int h = 0; h < 2; ++h) a_regs[h] *= static_cast<_Float16>(1.0f / N);
     const Stage3Folded s3{a, a3, lane};
+    // Steps 2-6 of a transform; at C = 8 the DFT8 runs on the matrix cores.
+    [[maybe_unused]] const f16x4 a8 = dft8_mfma_operand(lane);
+    auto steps = [&](cpx (&v)[kB][4]) {
+        if constexpr (C == 8 && kConv1dDft8OnMfma)
+            mfma8_steps2to6_dft8mfma(
+                region, [&](int c, int r) { return w1[(c * 4 + r) * 64 + lane]; }, s3, a8, lane, v);
+        else
+            mfma_steps2to6<C, true>(region, w1, s3, lane, v);
+    };
 
     const long long ntiles = (static_cast<long long>(batch) + P::kFPB - 1) / P::kFPB;
     long long tile, tile_end, step;
@@ -348,7 +365,7 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
     };
     auto forward = [&](cpx (&v)[kB][4]) {
         mfma_stage1_lds<C>(region, a, lane, v);
-        mfma_steps2to6<C, true>(region, w1, s3, lane, v);
+        steps(v);
     };
 
     unsigned hp[kB][4];  // FFT(h), packed half2
@@ -370,7 +387,7 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
         }
         wave_lds_sync();
         mfma_stage1_lds<C>(region, a, lane, v);
-        mfma_steps2to6<C, true>(region, w1, s3, lane, v);
+        steps(v);
         keep(v);
     }
 
@@ -440,7 +457,7 @@ conv1d_mfma_kernel(const __half2* __restrict__ x, const __half2* __restrict__ h,
             load(h + offset(tile + step), tile + step < tile_end ? valid(tile + step) : 0, rh);
         // ---- inverse = conj(DFT(conj(product))) / N, stage 1 from the registers ----
         mfma_stage1_regs<C, true>(a_regs, v);
-        mfma_steps2to6<C, true>(region, w1, s3, lane, v);
+        steps(v);
         // ---- store: block (f, m), lane (n, q) holds y_f[n + 16 m + 16C (q + 4 r)] ----
         wave_lds_sync();
 #pragma unroll

@@ -381,6 +381,102 @@ __device__ __forceinline__ void mfma_steps2to6(unsigned* region, const cpx* w1, 
         region, [&](int c, int r) { return w1[(c * 4 + r) * 64 + lane]; }, s3, lane, y);
 }
 
+// ---------------------------------------------------------------------------
+// Steps 2-6 of the N = 2048 plan (C = 8, one transform per wave) with the
+// DFT8 over c on the matrix cores instead of in-lane VALU butterflies.
+//   2. y[c][r] *= w1(c, r), rounded to half2 (the multiply fused with the
+//      rounding);
+//   3. for each r, a 4 x 4 transpose of 8-byte chunks across the wave's four
+//      16-lane rows (two v_permlane32_swap and two v_permlane16_swap per
+//      dword): lane (n, q) then holds, for each j, inputs c = 2q, 2q + 1 of
+//      the sequence (n, k1 = j + 4 r) -- the B operand of
+//      v_mfma_f32_16x16x16_f16, whose 16 columns are the 16 n of one k1 and
+//      whose A operand is the DFT8 matrix (dft8_mfma_operand); lane (n, q)
+//      receives outputs m = 2q, 2q + 1 of its column;
+//   4. (W_128^(n m) folded into S3's operands: S3 must be Stage3Folded);
+//   5. the transpose of mfma_steps2to6 (tpos), with block m at 256 m +
+//      4 floor((m + 2) / 4) (mfma8_block_base): the blocks do not overlap and
+//      the two 16-lane rows of a half-wave, which write blocks 2q + i, are 4
+//      dwords apart mod 8, so their dword writes fall on different banks;
+//   6. DFT16 over n, as mfma_steps2to6.
+// Forward direction only (the convolutions run their inverse as
+// conj(DFT(conj(x)))).  The data is rounded to f16 once more than with the
+// in-lane DFT8 (before the DFT8 instead of after it).
+using f16x4 = _Float16 __attribute__((ext_vector_type(4)));
+
+// Forward DFT8 A operand of v_mfma_f32_16x16x16_f16 for this lane: lane
+// (i, q) holds A[i][4 q + e]; row i = 2 m + o is output m, part o; column
+// 2 c + p is input c, part p.
+__device__ __forceinline__ f16x4 dft8_mfma_operand(int lane) {
+    const int i = lane & 15, q = lane >> 4;
+    const int m = i >> 1, o = i & 1;
+    f16x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int c = 2 * q + (e >> 1), p = e & 1;
+        const int ang = (2 * m * c) & 15;  // W_8^(m c) = W_16^(2 m c)
+        const float cs = kCos16[ang], sn = -kSin16[ang];
+        r[e] = static_cast<_Float16>(o == 0 ? (p == 0 ? cs : -sn) : (p == 0 ? sn : cs));
+    }
+    return r;
+}
+
+// Offset of block b in the C = 8 step-5 layout, added to tpos / tchunk
+// (0, 0, 4, 4, 4, 4, 8, 8 dwords; the region holds 2048 + 8).
+__device__ __forceinline__ int mfma8_block_base(int b) { return 4 * ((b + 2) >> 2); }
+
+template <class W1, class S3>
+__device__ __forceinline__ void mfma8_steps2to6_dft8mfma(unsigned* region, W1 w1, const S3& s3,
+                                                         f16x4 a8, int lane, cpx (&y)[8][4]) {
+    static_assert(!S3::kTwiddle, "step 4 must be folded into the stage-3 operands");
+    static_assert(MfmaPlan<8>::kRegion >= 2048 + 8, "region holds the shifted blocks");
+    const int n = lane & 15, q = lane >> 4;
+    f32x4 d[4][4];  // [r][j]: outputs m = 2q, 2q + 1 of the sequence (n, k1 = j + 4 r)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        unsigned pk[8];  // input c of the lane's sequence k1 = q + 4 r, half2
+#pragma unroll
+        for (int c = 0; c < 8; ++c) pk[c] = pack_half2(cmul(y[c][r], w1(c, r)));
+        unsigned t[4][2];  // t[j][h]: dword h of the chunk for instance k1 = j + 4 r
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            // chunk j (inputs 2j, 2j + 1) of row q goes to row j
+            const auto s02 = __builtin_amdgcn_permlane32_swap(pk[h], pk[4 + h], false, false);
+            const auto s13 = __builtin_amdgcn_permlane32_swap(pk[2 + h], pk[6 + h], false, false);
+            const auto t01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+            const auto t23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+            t[0][h] = t01[0];
+            t[1][h] = t01[1];
+            t[2][h] = t23[0];
+            t[3][h] = t23[1];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            d[r][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                a8, __builtin_bit_cast(f16x4, u32x2{t[j][0], t[j][1]}), f32x4{0.f, 0.f, 0.f, 0.f},
+                0, 0, 0);
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int m = 2 * q + i;
+                region[mfma8_block_base(m) + tpos(m, j + 4 * r, n)] =
+                    pack_half2(cpx{d[r][j][2 * i], d[r][j][2 * i + 1]});
+            }
+    wave_lds_sync();
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(region + mfma8_block_base(b) + tchunk(b, n, q));
+        f16x8 op[2];
+        s3.operands(b, op);
+        dft16_block(op, as_f16x8(x), y[b]);
+    }
+}
+
 // Steps 1-6 for the kFPW transforms a wave has staged in `region`, with the
 // workgroup set-up of mfma_setup and the stage-3 form S3.
 template <int C, bool FWD, class S3>
