@@ -18,7 +18,8 @@ transform) of the float forward transform; the inverse and the half
 transforms are measured the same way and reported under "also".  Each leg
 allocates its output right after its input; also.placement_*_n1024 repeats
 the forward transform with the output at 8 offsets inside one allocation,
-since the fp16 kernels' time depends on where the output lies.
+since the time of the fp16 kernels that walk many tiles per workgroup (the
+convolutions and the N = 2048, 4096 C2C) depends on where the output lies.
 
 roofline.achieved = algorithmic bytes per launch (read + write of every
 complex value once: 2 * batch * N * sizeof(T)) / the mean launch duration
@@ -326,11 +327,13 @@ def placement_spread(T: str, steps: int, warmup: int,
                      offsets_mib=(0, 32, 64, 96, 128, 160, 192, 224)) -> dict:
     """The C2C of the main workload (N=1024 x 65536 forward) with its output
     placed at x + (buffer size) + d MiB inside one allocation, for each d in
-    offsets_mib.  On MI355X the fp16 MFMA kernels' time depends on where the
-    output lies relative to the input (a pattern repeating every 128 MiB of d,
-    and differing between processes for the same d: the physical pages
-    differ); the fp32 kernel's does not.  The spread bounds what a single
-    placement, such as the other legs', can read."""
+    offsets_mib.  On MI355X the time of the fp16 MFMA kernels that walk many
+    tiles per workgroup depends on where the output lies relative to the
+    input (a pattern repeating every 128 MiB of d, and differing between
+    processes for the same d: the physical pages differ); the fp32 kernel's
+    does not, nor does the fp16 one-shot kernel's that this leg now runs at
+    N = 1024.  The spread bounds what a single placement, such as the other
+    legs', can read."""
     import torch
 
     import thunderfft_amd as thff

@@ -692,6 +692,81 @@ c2c_mfma_kernel(const __half2* __restrict__ in,
 
 namespace thff {
 
+// One-shot form of c2c_mfma_kernel: every wave moves one tile of kFPW
+// transforms and exits, as a streaming copy does (the dispatcher then keeps
+// the CUs evenly fed), with no LDS table and no workgroup barrier: the
+// lane's DFT16 operands come from the constant table and its 16 + (C - 1)
+// twiddles are computed with the hardware sine and cosine (cis_rev, accurate
+// to far below the f16 rounding the data takes), so nothing but the data
+// touches memory.  The wave's loads are issued before the coefficients are
+// computed.  Grid: one 256-lane workgroup per four tiles.
+template <int C, bool FWD, int kWaves = 4>
+__global__ __launch_bounds__(64 * kWaves) void c2c_mfma_wave_kernel(const __half2* __restrict__ in,
+                                                                    __half2* __restrict__ out,
+                                                                    int batch) {
+    using P = MfmaPlan<C>;
+    constexpr int N = P::N;
+    constexpr int kB = P::kBlocks;
+    constexpr int kRaw = P::kVals / 4;
+    __shared__ unsigned lds[kWaves * P::kRegion];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int n = lane & 15, q = lane >> 4;
+    unsigned* region = lds + wave * P::kRegion;
+    const long long first = (static_cast<long long>(blockIdx.x) * kWaves + wave) * P::kFPW;  // transform
+    const long long v = (static_cast<long long>(batch) - first) * N;
+    const int nv = v <= 0 ? 0 : (v >= P::kWaveVals ? P::kWaveVals : static_cast<int>(v));
+    if (nv == 0) return;  // uniform over the wave; no workgroup barrier follows
+    const __half2* src = in + first * N;
+    u32x4 cur[kRaw];
+#pragma unroll
+    for (int i = 0; i < kRaw; ++i) {
+        const int e = 4 * lane + 256 * i;
+        cur[i] = e < nv ? ld_nt(reinterpret_cast<const u32x4*>(src + e)) : u32x4{};
+    }
+    f16x8 a[2];
+    dft16_operands<FWD>(a, lane);
+    cpx w1[C * 4], w2[C > 1 ? C - 1 : 1];
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const cpx x = cis_rev((16 * c + n) * (q + 4 * r), N);
+            w1[c * 4 + r] = FWD ? cpx{x.re, -x.im} : x;
+        }
+#pragma unroll
+    for (int m = 1; m < C; ++m) {
+        const cpx x = cis_rev(16 * n * m, N);
+        w2[m - 1] = FWD ? cpx{x.re, -x.im} : x;
+    }
+#pragma unroll
+    for (int i = 0; i < kRaw; ++i)
+        *reinterpret_cast<u32x4*>(region + P::in_pad(4 * lane + 256 * i)) = cur[i];
+    wave_lds_sync();
+    cpx y[kB][4];
+    mfma_stage1_lds<C>(region, a, lane, y);
+    mfma_steps2to6_w<C, FWD>(region, [&](int c, int r) { return w1[c * 4 + r]; },
+                             Stage3Plain<false>{a, w2}, lane, y);
+    wave_lds_sync();
+#pragma unroll
+    for (int b = 0; b < kB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            region[P::out_pad((b / C) * N + n + 16 * (b % C) + P::kM * (q + 4 * r))] = pack_half2(y[b][r]);
+    wave_lds_sync();
+    __half2* dst = out + first * N;
+#pragma unroll
+    for (int i = 0; i < kRaw; ++i) {
+        const int e = 4 * lane + 256 * i;
+        if (e < nv)
+            st_nt(reinterpret_cast<u32x4*>(dst + e), *reinterpret_cast<const u32x4*>(region + P::out_pad(e)));
+    }
+}
+
+}  // namespace thff
+
+namespace thff {
+
 // ---------------------------------------------------------------------------
 // half2 C2C of N = 4096 = 16 x 16 x 16 on MFMA, one transform per workgroup
 // tile (4 waves, 16 values per lane).  With n = t0 + 16 t1 + 256 j and

@@ -52,12 +52,14 @@ inline Grid make_grid(long long ntiles, int per_cu, int num_cus) {
 //   fp16 N = 128 (MFMA, c2c_mfma128_kernel): 2 per CU with prefetch 87.3 us,
 //     against 90.0 at 3 per CU, 99.5 with one tile per workgroup and 90.3-91.1
 //     for the VALU kernel (one tile per workgroup; device grids 93).
-//   fp16 N = 256: one tile per workgroup, 86.0-88.7 us wherever the output
-//     lies; the 2-per-CU grid-stride walk with prefetch is as fast only for
-//     some output placements (86.3-103 us over 12 offsets of y from x, one
-//     box; N = 128, 512, 1024 keep the walk: one tile per workgroup took
-//     98-114 us for them, the per-tile table set-up included).
-//   fp16 MFMA: 2 per CU with prefetch, 86-91 us.  Runs
+//   fp16 N = 256 ... 1024: the one-shot kernel (kHalfOneShot below), whose
+//     shape is fixed there.  Before it, with the table-based kernel: N = 256
+//     one tile per workgroup, 86.0-88.7 us wherever the output lies; the
+//     2-per-CU grid-stride walk with prefetch as fast only for some output
+//     placements (86.3-103 us over 12 offsets of y from x, one box); N = 512,
+//     1024 on the walk (one tile per workgroup took 98-114 us for them, the
+//     per-tile table set-up included).
+//   fp16 MFMA (the walk): 2 per CU with prefetch, 86-91 us.  Runs
 //     of contiguous tiles per workgroup, which leave the balancing to the
 //     dispatcher, are slower: 2 tiles 87-98 us, 4-32 tiles 93-110 us (the
 //     grid-stride walk keeps all workgroups on neighbouring tiles).
@@ -100,12 +102,41 @@ void enqueue(Grid g, const IO* x, IO* y, int batch, const float2* tw, hipStream_
         x, y, batch, tw, g.tiles_per_block);
 }
 
+// fp16 N = 256 ... 1024 run the one-shot kernel (c2c_mfma_wave_kernel: one
+// tile per wave, the wave's twiddles computed in the kernel, no LDS table,
+// no workgroup barrier) instead of the persistent 2-per-CU grid-stride
+// kernel (c2c_mfma_kernel, whose workgroups build LDS tables once and walk
+// many tiles).  2^26 values, same output buffer, alternating (MI355X):
+// N = 1024 86.6-87.0 against 88.4-89.1 us, 512 86.4-87.0 against 86.8-87.6,
+// 256 85.7-86.4 against 86.5-87.6; over 8 output placements (bench.py's
+// placement leg) 86.9-88.4 us against 90.0-102.0 us at N = 1024: the
+// dispatcher keeps the CUs evenly fed, as for a streaming copy, and the
+// time no longer depends on where the output lies.  Workgroups of 1 or 2
+// such waves: 86.4-87.0 and 87.1-87.2 us at N = 1024, slower at 256 and 512.
+// The three-stage kernels (N = 2048, 4096) as one tile per workgroup with
+// computed twiddles took 128.3-128.8 and 94.7-95.1 us against 89.3-89.9 and
+// 89.5-89.9 us, so they keep the persistent walk.
+template <int N>
+inline constexpr bool kHalfOneShot = N >= 256 && N <= 1024;
+inline constexpr int kHalfOneShotWaves = 4;  // waves (tiles) per workgroup
+
 template <int N, bool FWD>
 void enqueue_mfma(Grid g, const __half2* x, __half2* y, int batch, const float2* tw,
                   hipStream_t stream) {
-    constexpr bool kPf = launch_shape<N>(1).prefetch;
-    c2c_mfma_kernel<N / 256, FWD, kPf><<<g.blocks, 256, 0, stream>>>(x, y, batch, tw,
-                                                                     g.tiles_per_block);
+    if constexpr (kHalfOneShot<N>) {
+        constexpr int kW = kHalfOneShotWaves;
+        constexpr long long kPerBlock = static_cast<long long>(kW) * MfmaPlan<N / 256>::kFPW;
+        const long long blocks = (static_cast<long long>(batch) + kPerBlock - 1) / kPerBlock;
+        if (blocks <= 0) return;
+        c2c_mfma_wave_kernel<N / 256, FWD, kW><<<static_cast<unsigned>(blocks), 64 * kW, 0, stream>>>(
+            x, y, batch);
+        (void)g;
+        (void)tw;
+    } else {
+        constexpr bool kPf = launch_shape<N>(1).prefetch;
+        c2c_mfma_kernel<N / 256, FWD, kPf><<<g.blocks, 256, 0, stream>>>(x, y, batch, tw,
+                                                                         g.tiles_per_block);
+    }
 }
 
 template <bool FWD>
